@@ -1,0 +1,112 @@
+/*
+ * mi355x_bench.h - C ABI of libmi355x_bench.so, the gfx950 (AMD Instinct
+ * MI355X) kernels behind the peak-throughput suite.
+ *
+ * The reference suite launches Triton kernels through `kernel[grid](...)` and
+ * reads compiled-kernel metadata from the returned object. This library
+ * replaces that boundary with plain C entry points that take device pointers,
+ * sizes and a HIP stream (passed as `void*`, NULL = the default stream).
+ * Each declaration names the reference interface it replaces.
+ *
+ * Conventions:
+ *   - return MB_OK (0) on success, a negative MB_ERR_* code on failure, and
+ *     never abort, throw or exit; mb_last_error() returns the message of the
+ *     calling thread's most recent failure;
+ *   - all device memory is allocated and owned by the caller;
+ *   - launches are asynchronous on `stream`; nothing here synchronises;
+ *   - one launch = one pass of the kernel over the caller's buffers.
+ */
+#ifndef MI355X_BENCH_H
+#define MI355X_BENCH_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MB_ABI_VERSION 1
+
+#define MB_OK 0
+#define MB_ERR_INVALID (-1)     /* bad argument: size, shape, configuration */
+#define MB_ERR_UNSUPPORTED (-2) /* valid request this library has no path for */
+#define MB_ERR_HIP (-3)         /* the HIP runtime reported an error */
+#define MB_ERR_ALIGNMENT (-4)   /* pointer alignment does not fit the kernel */
+
+/* ---- library and device ------------------------------------------------- */
+
+/* ABI version of the loaded library (MB_ABI_VERSION at build time). */
+int mb_abi_version(void);
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char* mb_last_error(void);
+
+typedef struct mb_device_info {
+  char name[256];           /* marketing name (hipDeviceProp_t.name) */
+  char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;    /* multiProcessorCount */
+  int32_t wavefront_size;   /* 64 on CDNA */
+  int32_t clock_khz;        /* peak engine clock reported by the runtime */
+  int32_t memory_clock_khz; /* memory clock reported by the runtime */
+  int32_t memory_bus_bits;  /* memory bus width */
+  int32_t reserved0;
+  int64_t l2_cache_bytes;   /* L2 size as HIP reports it (one XCD's L2) */
+  int64_t lds_bytes_per_cu; /* maxSharedMemoryPerMultiProcessor */
+  int64_t total_memory_bytes; /* hipMemGetInfo total */
+  int64_t free_memory_bytes;  /* hipMemGetInfo free */
+} mb_device_info;
+
+/* Device metadata for the setup block of every result document.
+ * Replaces: common.py:214-292 (setup_device) and bench_suite.py:106-114
+ * (probe_device), which read torch/Triton device properties and fall back to
+ * mem_get_info() for total memory (common.py:254-259). */
+int mb_device_query(int device, mb_device_info* out);
+
+typedef struct mb_kernel_attributes {
+  int32_t registers_per_thread; /* hipFuncAttributes.numRegs */
+  int32_t max_threads_per_block;
+  int64_t lds_bytes;            /* static group segment (sharedSizeBytes) */
+  int64_t scratch_bytes;        /* private segment per lane (localSizeBytes) */
+} mb_kernel_attributes;
+
+/* Number of registered kernels and their stable names. */
+int mb_kernel_count(void);
+const char* mb_kernel_name(int index);
+
+/* Runtime attributes of a registered kernel. Replaces the Triton
+ * CompiledKernel metadata the reference audits: n_regs, n_spills and
+ * metadata.shared (bench_tensor.py:1134-1136, bench_vector.py:625-627). */
+int mb_kernel_attributes_query(const char* name, mb_kernel_attributes* out);
+
+/* ---- memory: copy and read ---------------------------------------------- */
+
+/* Flags for mb_copy. */
+#define MB_COPY_NONTEMPORAL 1u /* streaming (nt) loads and stores */
+
+/* dst[0:bytes) = src[0:bytes): a coalesced 16-byte-per-lane copy.
+ * `block_threads` is a multiple of 64 up to 1024; each workgroup moves
+ * `block_threads * vectors_per_thread * 16` bytes per step. `grid_blocks` = 0
+ * launches one workgroup per step (the reference's grid = cdiv(N, BLOCK));
+ * otherwise that many workgroups stride over the buffer. A tail shorter than
+ * 16 bytes, or pointers without 16-byte alignment, take narrower accesses.
+ * Replaces: bench_bandwidth.py:36-47 (copy_kernel, launch_copy). */
+int mb_copy(const void* src, void* dst, uint64_t bytes, uint32_t block_threads,
+            uint32_t vectors_per_thread, uint32_t grid_blocks, uint32_t flags, void* stream);
+
+/* Element types understood by mb_read_sum. */
+#define MB_DTYPE_F32 0
+#define MB_DTYPE_F16 1
+#define MB_DTYPE_BF16 2
+
+/* sink[i] = sum(float(src[i*block_elements : (i+1)*block_elements])), the last
+ * segment clipped at `elements`; sink has cdiv(elements, block_elements)
+ * float32 entries. `block_elements` is a power of two between 64 and 65536.
+ * Replaces: bench_bandwidth.py:50-67 (read_kernel, launch_read). */
+int mb_read_sum(int dtype, const void* src, float* sink, uint64_t elements,
+                uint32_t block_elements, uint32_t block_threads, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_BENCH_H */

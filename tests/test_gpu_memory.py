@@ -1,0 +1,119 @@
+"""GPU parity of the memory kernels (mb_copy, mb_read_sum) against oracle.memory.
+
+Copy is bit-exact; block sums stay within the reference's float32 summation
+bound (bench_bandwidth.py:81-110). Cases cover ragged sizes, every access
+width (16-byte, dword, byte), misaligned pointers, grid-stride launches and the
+BASELINE size of 2^28 fp32 through size-independent properties.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import memory
+
+pytestmark = pytest.mark.gpu
+
+
+def _uniform(torch, n, seed, dtype=None, device="cuda"):
+    generator = torch.Generator(device=device)
+    generator.manual_seed(seed)
+    return torch.empty(n, device=device, dtype=dtype or torch.float32).uniform_(-1, 1, generator=generator)
+
+
+def _bits(tensor):
+    return tensor.cpu().contiguous().view(-1).numpy().view(np.uint8)
+
+
+@pytest.mark.parametrize("elements", [1, 3, 63, 64, 1000, 4096 + 17, (1 << 20) + 5])
+@pytest.mark.parametrize("vpt,nontemporal", [(1, False), (4, True), (16, False)])
+def test_copy_ragged_sizes_bit_exact(gpu, elements, vpt, nontemporal):
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import launch_copy
+
+    print(f"copy elements={elements} vpt={vpt} nt={nontemporal}", flush=True)
+    src = _uniform(torch, elements, seed=elements)
+    dst = torch.full_like(src, float("nan"))
+    launch_copy(src, dst, 256, vpt, 0, nontemporal)
+    torch.cuda.synchronize()
+    assert (_bits(dst) == _bits(torch.from_numpy(memory.copy(src.cpu().numpy())))).all()
+
+
+@pytest.mark.parametrize("offset_bytes", [4, 1, 3])
+def test_copy_misaligned_pointers_take_narrow_accesses(gpu, offset_bytes):
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+
+    print(f"misaligned copy offset={offset_bytes}", flush=True)
+    raw = torch.randint(0, 256, (1 << 16,), dtype=torch.uint8, device="cuda")
+    out = torch.zeros_like(raw)
+    count = (1 << 16) - 64
+    _native.call("mb_copy", raw.data_ptr() + offset_bytes, out.data_ptr() + offset_bytes, count, 256, 2, 0, 0,
+                 _native.stream_handle())
+    torch.cuda.synchronize()
+    got, want = out.cpu().numpy(), raw.cpu().numpy()
+    assert (got[offset_bytes:offset_bytes + count] == want[offset_bytes:offset_bytes + count]).all()
+    assert not got[:offset_bytes].any() and not got[offset_bytes + count:].any()  # nothing outside the range
+
+
+@pytest.mark.parametrize("grid_blocks", [1, 7, 512])
+def test_copy_grid_stride_covers_every_vector(gpu, grid_blocks):
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import launch_copy
+
+    print(f"grid-stride copy grid={grid_blocks}", flush=True)
+    src = _uniform(torch, (3 << 18) + 9, seed=grid_blocks)
+    dst = torch.full_like(src, float("nan"))
+    launch_copy(src, dst, 512, 2, grid_blocks, False)
+    torch.cuda.synchronize()
+    assert torch.equal(src.view(torch.int32), dst.view(torch.int32))
+
+
+def test_copy_baseline_size_full_buffer(gpu):
+    """2^28 fp32 (1 GiB): full bit equality on the device plus an oracle sample."""
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import launch_copy
+
+    print("copy 2^28 fp32", flush=True)
+    src = _uniform(torch, 1 << 28, seed=0)
+    dst = torch.full_like(src, float("nan"))
+    launch_copy(src, dst, 256, 4, 0, True)
+    torch.cuda.synchronize()
+    assert torch.equal(src.view(torch.int32), dst.view(torch.int32))
+    head, tail = slice(0, 1 << 16), slice((1 << 28) - (1 << 16), 1 << 28)
+    for part in (head, tail):
+        assert (_bits(dst[part]) == _bits(torch.from_numpy(memory.copy(src[part].cpu().numpy())))).all()
+    del src, dst
+
+
+@pytest.mark.parametrize("dtype_name", ["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("block", [64, 1024, 16384])
+@pytest.mark.parametrize("elements", [1, 1000, 65536 + 17])
+def test_read_block_sums_within_reference_bound(gpu, dtype_name, block, elements):
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import launch_read, torch_dtype
+
+    print(f"read {dtype_name} block={block} elements={elements}", flush=True)
+    src = _uniform(torch, elements, seed=block + elements, dtype=torch_dtype(dtype_name))
+    sink = torch.full((-(-elements // block),), float("nan"), device="cuda")
+    launch_read(src, sink, block, 256)
+    torch.cuda.synchronize()
+    memory.check_read(src.float().cpu().numpy(), sink.cpu().numpy(), block)
+
+
+def test_read_exact_on_integer_lattice(gpu):
+    """Small integers sum exactly in float32: any dropped or doubled element shows."""
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import launch_read
+
+    values = torch.randint(-8, 9, ((1 << 20) + 3,), device="cuda").float()
+    sink = torch.full((-(-values.numel() // 4096),), float("nan"), device="cuda")
+    launch_read(values, sink, 4096, 512)
+    torch.cuda.synchronize()
+    expected = memory.block_sums(values.cpu().numpy(), 4096)
+    assert np.array_equal(sink.cpu().numpy().astype(np.float64), expected)

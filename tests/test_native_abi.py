@@ -1,0 +1,70 @@
+"""The C-ABI library loads, and exports exactly what include/*.h declares.
+
+CPU-only: no entry point that launches work is called here.
+"""
+
+from pathlib import Path
+import re
+
+import pytest
+
+from triton_chip_benchmarks_amd import _native
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions():
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for match in re.finditer(r"\b(mb_[a-z0-9_]+)\s*\(", text):
+            names.add(match.group(1))
+    return names
+
+
+def test_headers_exist_and_declare_entry_points():
+    assert HEADERS, "include/*.h must declare the C-ABI"
+    assert {"mb_copy", "mb_read_sum", "mb_device_query", "mb_last_error"} <= declared_functions()
+
+
+def test_library_exports_every_declared_symbol():
+    library = _native.load()
+    missing = [name for name in sorted(declared_functions()) if not hasattr(library, name)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_python_binding_covers_exactly_the_header():
+    assert set(_native.SIGNATURES) == declared_functions()
+
+
+def test_abi_version_and_error_channel():
+    library = _native.load()
+    assert library.mb_abi_version() == _native.ABI_VERSION
+    assert isinstance(_native.last_error(), str)
+
+
+def test_kernel_registry_names_are_unique_and_cover_the_memory_kernels():
+    names = _native.kernel_names()
+    assert len(names) == len(set(names))
+    assert {"copy_dwordx4_vpt4_nt", "copy_tail", "read_sum_f32_vec"} <= set(names)
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    # Argument checks run on the host before the HIP runtime is touched.
+    library = _native.load()
+    assert library.mb_copy(None, None, 64, 256, 4, 0, 0, None) == _native.MB_ERR_INVALID
+    assert "NULL" in _native.last_error()
+    assert library.mb_copy(1 << 20, 2 << 20, 64, 100, 4, 0, 0, None) == _native.MB_ERR_INVALID
+    assert library.mb_copy(1 << 20, 2 << 20, 64, 256, 3, 0, 0, None) == _native.MB_ERR_INVALID
+    assert library.mb_copy(1 << 20, (1 << 20) + 16, 64, 256, 4, 0, 0, None) == _native.MB_ERR_INVALID
+    assert "overlap" in _native.last_error()
+    assert library.mb_read_sum(0, 1 << 20, 2 << 20, 100, 100, 256, None) == _native.MB_ERR_INVALID
+    assert library.mb_read_sum(7, 1 << 20, 2 << 20, 100, 1024, 256, None) == _native.MB_ERR_INVALID
+    assert library.mb_copy(None, None, 0, 256, 4, 0, 0, None) == _native.MB_OK  # empty copy is a no-op
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_native.NativeLibraryMissing):
+        _native.load(tmp_path / "absent.so")

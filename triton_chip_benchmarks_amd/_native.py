@@ -1,0 +1,158 @@
+"""ctypes binding of libmi355x_bench.so, the gfx950 C-ABI library.
+
+Every compute entry point of the suite goes through this module. There is no
+fallback: a missing or stale library raises NativeLibraryMissing, so a GPU run
+can never silently measure something other than the hand-written kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+import threading
+
+PACKAGE = Path(__file__).resolve().parent
+LIBRARY_PATH = PACKAGE / "libmi355x_bench.so"
+ABI_VERSION = 1
+
+MB_OK = 0
+MB_ERR_INVALID = -1
+MB_ERR_UNSUPPORTED = -2
+MB_ERR_HIP = -3
+MB_ERR_ALIGNMENT = -4
+
+MB_COPY_NONTEMPORAL = 1
+
+MB_DTYPE_F32 = 0
+MB_DTYPE_F16 = 1
+MB_DTYPE_BF16 = 2
+
+_ERROR_NAMES = {MB_ERR_INVALID: "invalid argument", MB_ERR_UNSUPPORTED: "unsupported",
+                MB_ERR_HIP: "HIP runtime error", MB_ERR_ALIGNMENT: "alignment"}
+
+
+class NativeLibraryMissing(RuntimeError):
+    """libmi355x_bench.so is absent, unloadable or built for another ABI."""
+
+
+class NativeError(RuntimeError):
+    """A C-ABI entry point returned a negative status."""
+
+    def __init__(self, code: int, message: str):
+        self.code = code
+        super().__init__(f"{_ERROR_NAMES.get(code, 'error')} ({code}): {message}")
+
+
+class UnsupportedNative(NativeError):
+    """MB_ERR_UNSUPPORTED: a valid request without an implemented path."""
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64),
+                ("compute_units", ctypes.c_int32), ("wavefront_size", ctypes.c_int32),
+                ("clock_khz", ctypes.c_int32), ("memory_clock_khz", ctypes.c_int32),
+                ("memory_bus_bits", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+                ("l2_cache_bytes", ctypes.c_int64), ("lds_bytes_per_cu", ctypes.c_int64),
+                ("total_memory_bytes", ctypes.c_int64), ("free_memory_bytes", ctypes.c_int64)]
+
+
+class KernelAttributes(ctypes.Structure):
+    _fields_ = [("registers_per_thread", ctypes.c_int32), ("max_threads_per_block", ctypes.c_int32),
+                ("lds_bytes", ctypes.c_int64), ("scratch_bytes", ctypes.c_int64)]
+
+
+_u64, _u32, _i32, _ptr = ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p
+
+# name -> (restype, argtypes). Every symbol here is declared in
+# include/mi355x_bench.h; tests check the two lists agree.
+SIGNATURES: dict[str, tuple[object, list]] = {
+    "mb_abi_version": (_i32, []),
+    "mb_last_error": (ctypes.c_char_p, []),
+    "mb_device_query": (_i32, [_i32, ctypes.POINTER(DeviceInfo)]),
+    "mb_kernel_count": (_i32, []),
+    "mb_kernel_name": (ctypes.c_char_p, [_i32]),
+    "mb_kernel_attributes_query": (_i32, [ctypes.c_char_p, ctypes.POINTER(KernelAttributes)]),
+    "mb_copy": (_i32, [_ptr, _ptr, _u64, _u32, _u32, _u32, _u32, _ptr]),
+    "mb_read_sum": (_i32, [_i32, _ptr, _ptr, _u64, _u32, _u32, _ptr]),
+}
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load the library once and bind every declared signature."""
+    global _library
+    with _lock:
+        if _library is not None and path is None:
+            return _library
+        target = Path(path) if path is not None else LIBRARY_PATH
+        if not target.exists():
+            raise NativeLibraryMissing(
+                f"{target} is missing; build it with `python -m triton_chip_benchmarks_amd.build` "
+                "(or __graft_entry__.build()) before running a benchmark")
+        try:
+            library = ctypes.CDLL(str(target))
+        except OSError as exc:
+            raise NativeLibraryMissing(f"cannot load {target}: {exc}") from exc
+        missing = []
+        for name, (restype, argtypes) in SIGNATURES.items():
+            function = getattr(library, name, None)
+            if function is None:
+                missing.append(name)
+                continue
+            function.restype = restype
+            function.argtypes = argtypes
+        if missing:
+            raise NativeLibraryMissing(f"{target} lacks {', '.join(missing)}; rebuild it")
+        version = library.mb_abi_version()
+        if version != ABI_VERSION:
+            raise NativeLibraryMissing(f"{target} has ABI {version}, expected {ABI_VERSION}; rebuild it")
+        if path is None:
+            _library = library
+        return library
+
+
+def last_error() -> str:
+    return (load().mb_last_error() or b"").decode(errors="replace")
+
+
+def check(status: int) -> None:
+    if status == MB_OK:
+        return
+    message = last_error()
+    if status == MB_ERR_UNSUPPORTED:
+        raise UnsupportedNative(status, message)
+    raise NativeError(status, message)
+
+
+def call(name: str, *arguments) -> None:
+    check(getattr(load(), name)(*arguments))
+
+
+def device_query(device: int) -> dict:
+    info = DeviceInfo()
+    call("mb_device_query", device, ctypes.byref(info))
+    return {field: (getattr(info, field).decode(errors="replace") if isinstance(getattr(info, field), bytes)
+                    else getattr(info, field)) for field, _ in DeviceInfo._fields_ if field != "reserved0"}
+
+
+def kernel_names() -> list[str]:
+    library = load()
+    return [library.mb_kernel_name(index).decode() for index in range(library.mb_kernel_count())]
+
+
+def kernel_attributes(name: str) -> dict:
+    attributes = KernelAttributes()
+    call("mb_kernel_attributes_query", name.encode(), ctypes.byref(attributes))
+    return {field: getattr(attributes, field) for field, _ in KernelAttributes._fields_}
+
+
+def stream_handle(stream=None) -> int | None:
+    """The raw hipStream_t of a torch stream (the current one by default)."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
+    return handle or None

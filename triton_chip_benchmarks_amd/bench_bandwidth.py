@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Peak HBM copy and read bandwidth on one MI355X with hand-written gfx950 kernels.
+
+Mirrors the reference's bench_bandwidth.py (bench_bandwidth.py:113-249): the
+same CLI, a masked-tail check per configuration, full-output validation of
+every measured buffer, the 4x-last-level-cache eligibility rule and the same
+row fields. Copy traffic is 2 x buffer bytes; read traffic is buffer bytes plus
+the float32 sink. The kernels are mb_copy (16-byte lanes) and mb_read_sum.
+"""
+
+from __future__ import annotations
+
+import argparse
+import math
+from pathlib import Path
+import sys
+
+if __package__ in (None, ""):
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    from triton_chip_benchmarks_amd import _native, roofline
+    from triton_chip_benchmarks_amd.common import (add_common_arguments, available_memory_bytes, emit_results,
+                                                   emit_unsupported, get_device, measure, positive_int,
+                                                   setup_device)
+else:
+    from . import _native, roofline
+    from .common import (add_common_arguments, available_memory_bytes, emit_results, emit_unsupported,
+                         get_device, measure, positive_int, setup_device)
+
+DTYPE_CODES = {"fp32": _native.MB_DTYPE_F32, "fp16": _native.MB_DTYPE_F16, "bf16": _native.MB_DTYPE_BF16}
+VECTOR_BYTES = 16
+WAVE = 64
+
+
+def torch_dtype(name):
+    import torch
+
+    return {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[name]
+
+
+def copy_geometry(block_size, element_size, num_warps):
+    """(threads, vectors per thread) of one workgroup step holding `block_size` elements."""
+    threads = WAVE * num_warps
+    vectors = block_size * element_size // VECTOR_BYTES
+    if vectors % threads:
+        return threads, None
+    per_thread = vectors // threads
+    return threads, per_thread if per_thread in (1, 2, 4, 8, 16) else None
+
+
+def launch_copy(src, dst, block_threads, vectors_per_thread, grid_blocks=0, nontemporal=False):
+    """dst <- src on the current stream through mb_copy."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("copy source and destination sizes differ")
+    _native.call("mb_copy", src.data_ptr(), dst.data_ptr(), nbytes, block_threads, vectors_per_thread,
+                 grid_blocks, _native.MB_COPY_NONTEMPORAL if nontemporal else 0, _native.stream_handle())
+
+
+def launch_read(src, sink, block_size, block_threads):
+    """sink[i] <- sum of src block i, through mb_read_sum."""
+    segments = -(-src.numel() // block_size)
+    if sink.numel() < segments:
+        raise ValueError(f"read sink holds {sink.numel()} sums, {segments} needed")
+    dtype = {"torch.float32": "fp32", "torch.float16": "fp16", "torch.bfloat16": "bf16"}[str(src.dtype)]
+    _native.call("mb_read_sum", DTYPE_CODES[dtype], src.data_ptr(), sink.data_ptr(), src.numel(), block_size,
+                 block_threads, _native.stream_handle())
+
+
+def check_read(src, sink, block_size):
+    """Validate every block sum against float64 (bench_bandwidth.py:81-110).
+
+    The float32 rounding of a sum of B values is bounded by its summation
+    depth times the sum of absolute values; the reference allows
+    2 * eps * log2(B) of it, plus 1e-6.
+    """
+    import torch
+
+    maximum_error, maximum_tolerance = 0.0, 0.0
+    rounding = 2 * torch.finfo(torch.float32).eps * max(1, math.log2(block_size))
+    chunk_elements = max(block_size, 1 << 20)
+    for start in range(0, src.numel(), chunk_elements):
+        chunk = src[start:start + chunk_elements]
+        rows = -(-chunk.numel() // block_size)
+        if chunk.numel() % block_size:
+            matrix = torch.zeros((rows, block_size), device=src.device, dtype=src.dtype)
+            matrix.view(-1)[:chunk.numel()].copy_(chunk)
+        else:
+            matrix = chunk.view(-1, block_size)
+        reference = matrix.sum(dim=1, dtype=torch.float64)
+        tolerance = matrix.abs().sum(dim=1, dtype=torch.float64) * rounding + 1e-6
+        actual = sink[start // block_size:start // block_size + rows].double()
+        error = (actual - reference).abs()
+        if not torch.all(error <= tolerance).item():
+            raise AssertionError("Read reduction validation failed: non-finite or inaccurate output; "
+                                 f"max_abs_error={error.max().item():.6g}")
+        maximum_error = max(maximum_error, error.max().item())
+        maximum_tolerance = max(maximum_tolerance, tolerance.max().item())
+    return {"correctness": "passed (all block sums against FP64, plus masked tail)",
+            "max_abs_error": maximum_error, "max_abs_tolerance": maximum_tolerance,
+            "reference_device": str(src.device)}
+
+
+def parse_args(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    add_common_arguments(parser)
+    parser.add_argument("--mode", choices=["copy", "read", "all"], default="all",
+                        help="Access patterns to measure separately (default: all)")
+    parser.add_argument("--sizes-mib", type=positive_int, nargs="+", default=[256, 512, 1024, 2048],
+                        help="Size of EACH source/destination buffer in MiB")
+    parser.add_argument("--dtype", choices=["fp16", "bf16", "fp32"], default="fp32")
+    parser.add_argument("--block-sizes", type=positive_int, nargs="+", default=[1024, 4096, 16384],
+                        help="Elements per workgroup step (copy) or per block sum (read)")
+    parser.add_argument("--num-warps", type=positive_int, nargs="+",
+                        help="64-lane waves per workgroup (default: 4 8)")
+    parser.add_argument("--nontemporal", choices=("off", "on", "both"), default="both",
+                        help="Copy with streaming (nt) loads/stores (default: measure both)")
+    parser.add_argument("--grid-blocks", type=int, default=0,
+                        help="Copy workgroups striding over the buffer; 0 = one per step (default)")
+    parser.add_argument("--seed", type=int, default=0, help="Source RNG seed (uniform [-1, 1))")
+    parser.add_argument("--quick", action="store_true",
+                        help="Smoke check: 8 MiB, one configuration per mode; not an HBM result")
+    args = parser.parse_args(argv)
+    if args.quick:
+        args.sizes_mib, args.block_sizes, args.num_warps, args.nontemporal = [8], [1024], None, "off"
+    if any(block & (block - 1) or block > 65536 for block in args.block_sizes):
+        parser.error("--block-sizes must be powers of two no greater than 65536")
+    if args.num_warps is not None and any(warps not in (1, 2, 4, 8, 16) for warps in args.num_warps):
+        parser.error("--num-warps must be 1, 2, 4, 8 or 16")
+    if args.grid_blocks < 0:
+        parser.error("--grid-blocks must be non-negative")
+    return args
+
+
+def configurations(args, element_size):
+    warps = args.num_warps or ([4] if args.quick else [4, 8])
+    nontemporal = {"off": [False], "on": [True], "both": [False, True]}[args.nontemporal]
+    configs = []
+    for block in args.block_sizes:
+        for num_warps in warps:
+            threads, per_thread = copy_geometry(block, element_size, num_warps)
+            configs.append({"block_size": block, "num_warps": num_warps, "block_threads": threads,
+                            "vectors_per_thread": per_thread, "nontemporal": nontemporal})
+    return configs
+
+
+def main(argv=None):
+    import torch
+
+    args = parse_args(argv)
+    metadata = setup_device(args)
+    device = get_device(args)
+    dtype = torch_dtype(args.dtype)
+    element_size = torch.empty((), dtype=dtype).element_size()
+    cache_bytes = metadata["l2_cache_bytes"]
+    modes = ["copy", "read"] if args.mode == "all" else [args.mode]
+    configs = configurations(args, element_size)
+    generator = torch.Generator(device=device)
+
+    for config in configs:
+        block, threads = config["block_size"], config["block_threads"]
+        generator.manual_seed(args.seed)
+        small_src = torch.empty(block + 17, device=device, dtype=dtype).uniform_(-1, 1, generator=generator)
+        if "copy" in modes and config["vectors_per_thread"] is not None:
+            for nontemporal in config["nontemporal"]:
+                small_dst = torch.full_like(small_src, float("nan"))
+                launch_copy(small_src, small_dst, threads, config["vectors_per_thread"], args.grid_blocks,
+                            nontemporal)
+                if not torch.equal(small_src, small_dst):
+                    raise AssertionError(f"Copy tail validation failed: block={block}, warps={config['num_warps']}")
+        if "read" in modes:
+            small_sink = torch.full((-(-small_src.numel() // block),), float("nan"), device=device)
+            launch_read(small_src, small_sink, block, threads)
+            check_read(small_src, small_sink, block)
+    print("Validation: masked tails passed; every measured output is checked in full.")
+    print("Copy traffic = 2 * buffer bytes; read traffic = buffer bytes + FP32 reduction sink. "
+          "GB/s and TB/s use decimal units; peak uses the shortest timed sample.")
+    print("mode   buffer MiB   block  warps  nt      min ms   median ms   peak GB/s  median GB/s  % of 8 TB/s")
+    rows = []
+    for size_mib in args.sizes_mib:
+        buffer_bytes = size_mib * 2**20
+        n = buffer_bytes // element_size
+        free_bytes = available_memory_bytes()
+        max_sink = -(-n // min(args.block_sizes)) * 4 if "read" in modes else 0
+        required = (2 if "copy" in modes else 1) * buffer_bytes + max_sink
+        if free_bytes is not None and required + 512 * 2**20 > free_bytes:
+            raise SystemExit(f"Insufficient free GPU memory for {size_mib} MiB buffers; reduce --sizes-mib.")
+        regime = ("unknown_l2" if not cache_bytes else
+                  "larger_than_l2" if buffer_bytes >= 4 * cache_bytes else "cache_sensitive")
+        peak_eligible = regime == "larger_than_l2" and not args.quick
+        if not peak_eligible:
+            reason = ("smoke mode" if args.quick else "cache capacity is unavailable" if not cache_bytes
+                      else "buffer is smaller than 4x the last-level cache")
+            print(f"Note: {size_mib} MiB per buffer excluded from the HBM-sized peak summary: {reason}.")
+        generator.manual_seed(args.seed)
+        src = torch.empty(n, device=device, dtype=dtype).uniform_(-1, 1, generator=generator)
+        dst = torch.empty_like(src) if "copy" in modes else None
+        for config in configs:
+            block, warps, threads = config["block_size"], config["num_warps"], config["block_threads"]
+            for mode in modes:
+                variants = config["nontemporal"] if mode == "copy" else [None]
+                if mode == "copy" and config["vectors_per_thread"] is None:
+                    continue  # step size does not split into whole 16-byte lanes
+                for nontemporal in variants:
+                    sink = None
+                    if mode == "copy":
+                        per_thread = config["vectors_per_thread"]
+                        dst.fill_(float("nan"))
+
+                        def run(per_thread=per_thread, nontemporal=nontemporal, threads=threads):
+                            launch_copy(src, dst, threads, per_thread, args.grid_blocks, nontemporal)
+
+                        run()
+                        if not torch.equal(src, dst):
+                            raise AssertionError(f"Copy validation failed: size={size_mib}, block={block}, "
+                                                 f"warps={warps}, nt={nontemporal}")
+                        correctness = {"correctness": "passed (full output and masked tail)"}
+                        write_bytes = buffer_bytes
+                        kernel = f"copy_dwordx4_vpt{per_thread}{'_nt' if nontemporal else ''}"
+                    else:
+                        sink = torch.full((-(-n // block),), float("nan"), device=device)
+
+                        def run(block=block, threads=threads, sink=sink):
+                            launch_read(src, sink, block, threads)
+
+                        run()
+                        correctness = check_read(src, sink, block)
+                        write_bytes = sink.numel() * sink.element_size()
+                        kernel = f"read_sum_{args.dtype}_vec"
+                    timings = measure(run, args)
+                    traffic = buffer_bytes + write_bytes
+                    gbps = traffic / (timings["median_ms"] * 1e6)
+                    peak_gbps = traffic / (timings["min_ms"] * 1e6)
+                    row = {"mode": f"device_global_memory_{mode}", "pattern": mode, "dtype": args.dtype,
+                           "buffer_mib": size_mib, "buffer_bytes": buffer_bytes, "elements": n,
+                           "read_bytes": buffer_bytes, "write_bytes": write_bytes, "traffic_bytes": traffic,
+                           "block_size": block, "num_warps": warps, "block_threads": threads,
+                           "kernel": kernel, "cache_regime": regime, "peak_eligible": peak_eligible,
+                           "smoke_only": args.quick, **timings, "gbps": gbps, "tbps": gbps / 1000,
+                           "peak_gbps": peak_gbps, "peak_tbps": peak_gbps / 1000,
+                           "fraction_of_hbm_peak": peak_gbps / roofline.HBM_PEAK_GBPS, **correctness}
+                    if mode == "copy":
+                        row.update(vectors_per_thread=config["vectors_per_thread"], nontemporal=nontemporal,
+                                   grid_blocks=args.grid_blocks, seed=args.seed,
+                                   source_distribution="uniform[-1, 1)")
+                    rows.append(row)
+                    nt_label = "-" if nontemporal is None else ("on" if nontemporal else "off")
+                    print(f"{mode:4s} {size_mib:11d} {block:7d} {warps:6d} {nt_label:>3} "
+                          f"{timings['min_ms']:11.6f} {timings['median_ms']:11.6f} {peak_gbps:11.2f} "
+                          f"{gbps:12.2f} {100 * peak_gbps / roofline.HBM_PEAK_GBPS:11.1f}", flush=True)
+                    del sink
+        del src, dst
+    eligible = [row for row in rows if row["peak_eligible"]]
+    for mode in modes:
+        candidates = [row for row in (eligible or rows) if row["pattern"] == mode]
+        if not candidates:
+            continue
+        best = max(candidates, key=lambda row: row["peak_gbps"])
+        label = "Best measured" if eligible else "Best cache-sensitive/smoke"
+        print(f"{label} {mode} bandwidth: {best['peak_gbps']:.2f} GB/s ({best['peak_tbps']:.3f} TB/s, "
+              f"{100 * best['fraction_of_hbm_peak']:.1f}% of 8 TB/s), {best['buffer_mib']} MiB/buffer, "
+              f"block={best['block_size']}, warps={best['num_warps']}.")
+    if not eligible:
+        print("No HBM-sized peak candidate: eligibility requires buffers >= 4x the last-level cache "
+              "and a run without --quick.")
+    emit_results("bandwidth", metadata, args, rows)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,268 @@
+// HBM copy and read kernels (memory_bandwidth row).
+//
+// Copy: every lane moves 16-byte vectors (global_load_dwordx4 /
+// global_store_dwordx4); consecutive lanes touch consecutive vectors, so each
+// wave64 instruction covers 1 KiB of contiguous memory. A workgroup step holds
+// `vectors_per_thread` independent loads in flight before the stores, which is
+// what keeps enough bytes outstanding per CU to saturate HBM3E.
+//
+// Read: one wave reduces one segment of `block_elements` values to a single
+// float (the reference's per-program sum), streaming it with 16-byte loads and
+// eight independent accumulators, then a butterfly across the 64 lanes. The
+// summation depth stays below the 2*eps*log2(block) bound the reference
+// validates block sums with (bench_bandwidth.py:87).
+#include "mb_internal.h"
+
+namespace mb {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T, bool NT>
+__device__ __forceinline__ T load_elem(const T* ptr) {
+  if constexpr (NT) return __builtin_nontemporal_load(ptr);
+  return *ptr;
+}
+
+template <typename T, bool NT>
+__device__ __forceinline__ void store_elem(T* ptr, T value) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(value, ptr);
+  } else {
+    *ptr = value;
+  }
+}
+
+// T is the access unit (u32x4, uint32_t or uint8_t); n counts units.
+template <typename T, int VPT, bool NT>
+__global__ void __launch_bounds__(1024) copy_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                                     uint64_t n) {
+  const uint64_t threads = blockDim.x;
+  const uint64_t step = threads * VPT;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * step;
+  for (uint64_t base = blockIdx.x * step + threadIdx.x; base < n; base += stride) {
+    T values[VPT];
+    if (base + (VPT - 1) * threads < n) {
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) values[j] = load_elem<T, NT>(src + base + j * threads);
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) store_elem<T, NT>(dst + base + j * threads, values[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VPT; ++j)
+        if (base + j * threads < n) values[j] = load_elem<T, NT>(src + base + j * threads);
+#pragma unroll
+      for (int j = 0; j < VPT; ++j)
+        if (base + j * threads < n) store_elem<T, NT>(dst + base + j * threads, values[j]);
+    }
+  }
+}
+
+// Bytes after the last whole 16-byte vector.
+__global__ void copy_tail_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t n) {
+  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+}
+
+template <typename T>
+__device__ __forceinline__ float to_float(T value);
+template <>
+__device__ __forceinline__ float to_float<float>(float value) { return value; }
+template <>
+__device__ __forceinline__ float to_float<_Float16>(_Float16 value) { return static_cast<float>(value); }
+template <>
+__device__ __forceinline__ float to_float<uint16_t>(uint16_t bits) {  // bfloat16 bit pattern
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float value) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_xor(value, offset, 64);
+  return value;
+}
+
+// One wave per segment; waves stride over the segments of the buffer.
+// VEC elements per lane per load (16 bytes, or 1 for unaligned sources).
+template <typename T, int VEC>
+__global__ void __launch_bounds__(1024) read_sum_kernel(const T* __restrict__ src, float* __restrict__ sink,
+                                                         uint64_t elements, uint32_t block_elements,
+                                                         uint64_t segments) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t waves_per_block = blockDim.x >> 6;
+  const uint64_t wave = blockIdx.x * waves_per_block + (threadIdx.x >> 6);
+  const uint64_t total_waves = static_cast<uint64_t>(gridDim.x) * waves_per_block;
+  const uint32_t chunk = 64 * VEC;  // elements one wave covers per load
+  for (uint64_t segment = wave; segment < segments; segment += total_waves) {
+    const uint64_t first = segment * block_elements;
+    const uint64_t count = (elements - first < block_elements) ? elements - first : block_elements;
+    const T* base = src + first;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (count == block_elements && block_elements >= chunk) {
+      const uint32_t loads = block_elements / chunk;
+      for (uint32_t p = 0; p < loads; ++p) {
+        const T* ptr = base + p * chunk + lane * VEC;
+        if constexpr (VEC == 4 && sizeof(T) == 4) {
+          const float4 v = *reinterpret_cast<const float4*>(ptr);
+          acc[p & 7] += (v.x + v.y) + (v.z + v.w);
+        } else if constexpr (VEC == 8 && sizeof(T) == 2) {
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(ptr);
+          const T* h = reinterpret_cast<const T*>(&raw);
+          acc[p & 7] += ((to_float(h[0]) + to_float(h[1])) + (to_float(h[2]) + to_float(h[3]))) +
+                        ((to_float(h[4]) + to_float(h[5])) + (to_float(h[6]) + to_float(h[7])));
+        } else {
+          float partial = 0.f;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) partial += to_float(ptr[j]);
+          acc[p & 7] += partial;
+        }
+      }
+    } else {
+      // Clipped last segment, or a segment narrower than one vector load.
+      for (uint64_t i = lane; i < count; i += 64) acc[(i >> 6) & 7] += to_float(base[i]);
+    }
+    const float total =
+        wave_sum(((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])));
+    if (lane == 0) sink[segment] = total;
+  }
+}
+
+template <typename T, bool NT>
+int launch_copy_units(const void* src, void* dst, uint64_t units, uint32_t threads, uint32_t vpt,
+                      uint32_t grid_blocks, hipStream_t stream) {
+  const uint64_t step = static_cast<uint64_t>(threads) * vpt;
+  const uint64_t steps = (units + step - 1) / step;
+  uint64_t grid = grid_blocks ? (grid_blocks < steps ? grid_blocks : steps) : steps;
+  if (grid == 0) return MB_OK;
+  if (grid > 0x7fffffffull)
+    return fail(MB_ERR_INVALID, "mb_copy: %llu workgroups exceed the grid limit; raise vectors_per_thread",
+                static_cast<unsigned long long>(grid));
+  const T* s = static_cast<const T*>(src);
+  T* d = static_cast<T*>(dst);
+  dim3 g(static_cast<uint32_t>(grid)), b(threads);
+  switch (vpt) {
+    case 1: copy_kernel<T, 1, NT><<<g, b, 0, stream>>>(s, d, units); break;
+    case 2: copy_kernel<T, 2, NT><<<g, b, 0, stream>>>(s, d, units); break;
+    case 4: copy_kernel<T, 4, NT><<<g, b, 0, stream>>>(s, d, units); break;
+    case 8: copy_kernel<T, 8, NT><<<g, b, 0, stream>>>(s, d, units); break;
+    case 16: copy_kernel<T, 16, NT><<<g, b, 0, stream>>>(s, d, units); break;
+    default: return fail(MB_ERR_INVALID, "mb_copy: vectors_per_thread %u not in {1,2,4,8,16}", vpt);
+  }
+  return launch_status("copy_kernel");
+}
+
+#define MB_REGISTER_COPY(T, TNAME)                                                            \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt1", (copy_kernel<T, 1, false>));                     \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt2", (copy_kernel<T, 2, false>));                     \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt4", (copy_kernel<T, 4, false>));                     \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt8", (copy_kernel<T, 8, false>));                     \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt16", (copy_kernel<T, 16, false>));                   \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt1_nt", (copy_kernel<T, 1, true>));                   \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt2_nt", (copy_kernel<T, 2, true>));                   \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt4_nt", (copy_kernel<T, 4, true>));                   \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt8_nt", (copy_kernel<T, 8, true>));                   \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt16_nt", (copy_kernel<T, 16, true>))
+
+MB_REGISTER_COPY(u32x4, "dwordx4");
+MB_REGISTER_COPY(uint32_t, "dword");
+MB_REGISTER_COPY(uint8_t, "byte");
+MB_REGISTER_KERNEL("copy_tail", copy_tail_kernel);
+MB_REGISTER_KERNEL("read_sum_f32_vec", (read_sum_kernel<float, 4>));
+MB_REGISTER_KERNEL("read_sum_f32", (read_sum_kernel<float, 1>));
+MB_REGISTER_KERNEL("read_sum_f16_vec", (read_sum_kernel<_Float16, 8>));
+MB_REGISTER_KERNEL("read_sum_f16", (read_sum_kernel<_Float16, 1>));
+MB_REGISTER_KERNEL("read_sum_bf16_vec", (read_sum_kernel<uint16_t, 8>));
+MB_REGISTER_KERNEL("read_sum_bf16", (read_sum_kernel<uint16_t, 1>));
+
+template <typename T>
+int launch_read(const void* src, float* sink, uint64_t elements, uint32_t block_elements, uint32_t threads,
+                hipStream_t stream) {
+  constexpr int kVec = 16 / sizeof(T);
+  const uint64_t segments = (elements + block_elements - 1) / block_elements;
+  const uint64_t waves_per_block = threads / 64;
+  uint64_t grid = (segments + waves_per_block - 1) / waves_per_block;
+  // Waves stride over segments, so a bounded grid still covers every segment.
+  const uint64_t max_grid = 1ull << 20;
+  if (grid > max_grid) grid = max_grid;
+  const T* s = static_cast<const T*>(src);
+  dim3 g(static_cast<uint32_t>(grid)), b(threads);
+  if (aligned(src, 16) && block_elements >= 64u * kVec) {
+    read_sum_kernel<T, kVec><<<g, b, 0, stream>>>(s, sink, elements, block_elements, segments);
+  } else {
+    read_sum_kernel<T, 1><<<g, b, 0, stream>>>(s, sink, elements, block_elements, segments);
+  }
+  return launch_status("read_sum_kernel");
+}
+
+}  // namespace
+}  // namespace mb
+
+extern "C" {
+
+int mb_copy(const void* src, void* dst, uint64_t bytes, uint32_t block_threads, uint32_t vectors_per_thread,
+            uint32_t grid_blocks, uint32_t flags, void* stream) {
+  using namespace mb;
+  if (bytes == 0) return MB_OK;
+  if (src == nullptr || dst == nullptr) return fail(MB_ERR_INVALID, "mb_copy: NULL buffer");
+  if (block_threads == 0 || block_threads % 64 || block_threads > 1024)
+    return fail(MB_ERR_INVALID, "mb_copy: block_threads %u must be a multiple of 64 up to 1024", block_threads);
+  if (!power_of_two(vectors_per_thread) || vectors_per_thread > 16)
+    return fail(MB_ERR_INVALID, "mb_copy: vectors_per_thread %u not in {1,2,4,8,16}", vectors_per_thread);
+  if (flags & ~MB_COPY_NONTEMPORAL) return fail(MB_ERR_INVALID, "mb_copy: unknown flags 0x%x", flags);
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  if (s < d + bytes && d < s + bytes) return fail(MB_ERR_INVALID, "mb_copy: source and destination overlap");
+  const bool nt = flags & MB_COPY_NONTEMPORAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (aligned(src, 16) && aligned(dst, 16)) {
+    const uint64_t vectors = bytes / 16;
+    int rc = nt ? launch_copy_units<u32x4, true>(src, dst, vectors, block_threads, vectors_per_thread,
+                                                 grid_blocks, st)
+                : launch_copy_units<u32x4, false>(src, dst, vectors, block_threads, vectors_per_thread,
+                                                  grid_blocks, st);
+    if (rc) return rc;
+    const uint32_t tail = static_cast<uint32_t>(bytes % 16);
+    if (tail) {
+      copy_tail_kernel<<<1, 64, 0, st>>>(reinterpret_cast<const uint8_t*>(s + vectors * 16),
+                                         reinterpret_cast<uint8_t*>(d + vectors * 16), tail);
+      return launch_status("copy_tail_kernel");
+    }
+    return MB_OK;
+  }
+  if (aligned(src, 4) && aligned(dst, 4) && bytes % 4 == 0)
+    return nt ? launch_copy_units<uint32_t, true>(src, dst, bytes / 4, block_threads, vectors_per_thread,
+                                                  grid_blocks, st)
+              : launch_copy_units<uint32_t, false>(src, dst, bytes / 4, block_threads, vectors_per_thread,
+                                                   grid_blocks, st);
+  return nt ? launch_copy_units<uint8_t, true>(src, dst, bytes, block_threads, vectors_per_thread, grid_blocks, st)
+            : launch_copy_units<uint8_t, false>(src, dst, bytes, block_threads, vectors_per_thread, grid_blocks,
+                                                st);
+}
+
+int mb_read_sum(int dtype, const void* src, float* sink, uint64_t elements, uint32_t block_elements,
+                uint32_t block_threads, void* stream) {
+  using namespace mb;
+  if (elements == 0) return MB_OK;
+  if (src == nullptr || sink == nullptr) return fail(MB_ERR_INVALID, "mb_read_sum: NULL buffer");
+  if (!power_of_two(block_elements) || block_elements < 64 || block_elements > 65536)
+    return fail(MB_ERR_INVALID, "mb_read_sum: block_elements %u must be a power of two in [64, 65536]",
+                block_elements);
+  if (block_threads == 0 || block_threads % 64 || block_threads > 1024)
+    return fail(MB_ERR_INVALID, "mb_read_sum: block_threads %u must be a multiple of 64 up to 1024",
+                block_threads);
+  if (!aligned(sink, 4)) return fail(MB_ERR_ALIGNMENT, "mb_read_sum: sink must be 4-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MB_DTYPE_F32:
+      if (!aligned(src, 4)) return fail(MB_ERR_ALIGNMENT, "mb_read_sum: f32 source must be 4-byte aligned");
+      return launch_read<float>(src, sink, elements, block_elements, block_threads, st);
+    case MB_DTYPE_F16:
+      if (!aligned(src, 2)) return fail(MB_ERR_ALIGNMENT, "mb_read_sum: f16 source must be 2-byte aligned");
+      return launch_read<_Float16>(src, sink, elements, block_elements, block_threads, st);
+    case MB_DTYPE_BF16:
+      if (!aligned(src, 2)) return fail(MB_ERR_ALIGNMENT, "mb_read_sum: bf16 source must be 2-byte aligned");
+      return launch_read<uint16_t>(src, sink, elements, block_elements, block_threads, st);
+    default:
+      return fail(MB_ERR_INVALID, "mb_read_sum: unknown dtype %d", dtype);
+  }
+}
+
+}  // extern "C"
