@@ -3,15 +3,24 @@
 
 Metric: "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of
 MI355X peak". One step is one pass of the hot path over resident synthetic
-inputs: one launch of each headline kernel,
-  - HBM copy of 2^28 fp32 (1 GiB, uniform[-1,1) from a seed) into a second buffer,
-  - the resident-operand MFMA peak kernels (BF16, FP8 E4M3, MXFP4) when built.
-Every kernel's output is checked against the CPU oracle before timing. The K
-timed steps are bracketed by torch.cuda.synchronize(); per-kernel durations come
-from HIP events recorded around each launch on the launch stream.
+inputs - one launch of each headline kernel:
+  hbm_copy    mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from seed 0) into a
+              second buffer (memory_bandwidth row);
+  peak_bf16   mb_tensor_peak BF16, 128x128x64 tiles, 2 chains, 1024 MFMA
+              iterations, 2 workgroups per CU (tensor_bf16 row);
+  peak_fp8    the same with FP8 E4M3, 128x128x128 tiles (tensor_fp8 row);
+  peak_mxfp4  the same with MX FP4 E2M1 + E8M0 scales, 128x128x256 tiles
+              (tensor_fp4 row).
+Operands follow the reference's peak lattices (bench_tensor.py:614-672). Every
+kernel's output is validated before timing with the product's own checks
+(bit equality for the copy; exact float64 lattice references under the
+reference's tolerance for the MFMA rows). The K timed steps are bracketed by
+torch.cuda.synchronize(); per-kernel durations come from HIP events recorded
+around each launch on the launch stream.
 
-value = mean over the headline rows of (achieved rate / MI355X published peak),
-in percent. The per-row absolute rates are in "rows".
+value = mean over the headline rows of (achieved rate / MI355X published
+peak), in percent; the absolute rates are in "rows". The CPU baseline times
+the oracle (numpy) on bounded samples of the same work on the host.
 """
 
 from __future__ import annotations
@@ -29,9 +38,13 @@ sys.path.insert(0, str(ROOT))
 METRIC = "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of MI355X peak"
 COPY_ELEMENTS = 2**28
 COPY_SEED = 0
-# Copy launch shape chosen by the bench_bandwidth sweep on MI355X.
+# Launch shapes chosen from the bench_bandwidth / bench_tensor sweeps on MI355X.
 COPY_CONFIG = {"block_threads": 256, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": True}
+PEAK_ITERATIONS = 1024
+PEAK_BLOCKS_PER_CU = 2
+PEAK_TILES = {"bf16": (128, 128, 64), "fp8": (128, 128, 128), "fp4": (128, 128, 256)}
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_per_launch.txt"
+CPU_BUDGET_S = 4.0  # per row, so the default run stays within a few minutes
 
 
 def parse_args(argv=None):
@@ -41,34 +54,42 @@ def parse_args(argv=None):
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true",
                         help="Skip the timed CPU baseline leg (it is on by default)")
-    parser.add_argument("--rows", nargs="+", help="Subset of headline rows to run")
+    parser.add_argument("--rows", nargs="+", help="Subset of headline rows: hbm_copy peak_bf16 peak_fp8 peak_mxfp4")
     return parser.parse_args(argv)
 
 
-def _traffic_table() -> dict[str, float]:
-    """Measured HBM bytes per launch by kernel, from committed rocprofv3 summaries."""
+def traffic_table() -> dict[str, float]:
+    """Measured HBM bytes per launch by kernel (from committed rocprofv3 counter runs)."""
     table = {}
     if TRAFFIC_FILE.exists():
         for line in TRAFFIC_FILE.read_text().splitlines():
-            line = line.strip()
-            if not line or line.startswith("#") or "=" not in line:
-                continue
-            key, value = (part.strip() for part in line.split("=", 1))
-            try:
-                table[key] = float(value)
-            except ValueError:
-                continue
+            line = line.split("#", 1)[0].strip()
+            if "=" in line:
+                key, value = (part.strip() for part in line.split("=", 1))
+                try:
+                    table[key] = float(value)
+                except ValueError:
+                    pass
     return table
+
+
+def _best_of(fn, budget_s):
+    """Best wall time of repeated host calls within a time budget (CPU leg only)."""
+    fn()
+    best, spent = None, 0.0
+    while spent < budget_s or best is None:
+        start = time.perf_counter()
+        fn()
+        elapsed = time.perf_counter() - start
+        spent += elapsed
+        best = elapsed if best is None else min(best, elapsed)
+    return best
 
 
 class CopyWorkload:
     """memory_bandwidth row: 1 GiB fp32 device-to-device copy."""
 
-    name = "hbm_copy"
-    dtype = "f32"
-    metric_key = "memory_bandwidth"
-    unit = "GB/s"
-    bound = "hbm"
+    name, dtype, metric_key, unit, bound = "hbm_copy", "f32", "memory_bandwidth", "GB/s", "hbm"
 
     def __init__(self, torch):
         from triton_chip_benchmarks_amd import bench_bandwidth
@@ -82,56 +103,110 @@ class CopyWorkload:
         self.work = 2 * self.src.numel() * 4  # algorithmic bytes: read + write (bench_bandwidth.py:212)
         self.kernel = f"copy_dwordx4_vpt{COPY_CONFIG['vectors_per_thread']}" + (
             "_nt" if COPY_CONFIG["nontemporal"] else "")
+        self.config = {"elements": COPY_ELEMENTS, "dtype": "fp32", **COPY_CONFIG}
 
     def launch(self):
         self.launcher(self.src, self.dst, COPY_CONFIG["block_threads"], COPY_CONFIG["vectors_per_thread"],
                       COPY_CONFIG["grid_blocks"], COPY_CONFIG["nontemporal"])
 
     def validate(self):
-        from oracle import memory
-
         self.dst.fill_(float("nan"))
         self.launch()
         self.torch.cuda.synchronize()
-        # Bit-exact: compare raw bits on the device, then an oracle sample on the host.
         if not self.torch.equal(self.src.view(self.torch.int32), self.dst.view(self.torch.int32)):
-            raise AssertionError("copy output differs from source")
-        sample = self.src[:1 << 20].cpu().numpy()
-        expected = memory.copy(sample)
-        if not (self.dst[:1 << 20].cpu().numpy().view("u4") == expected.view("u4")).all():
-            raise AssertionError("copy sample differs from the oracle")
-        return "bit-exact: full buffer on device, 1 Mi-element sample against oracle.memory.copy"
+            raise AssertionError("copy output differs from its source")
+        return "bit-exact: every word of the 1 GiB destination equals the source"
 
-    def rate(self, ms_per_launch):
-        return self.work / (ms_per_launch * 1e6)  # GB/s
+    def rate(self, ms):
+        return self.work / (ms * 1e6)  # GB/s
 
-    def cpu_baseline(self):
-        """oracle.memory.copy of a 256 MiB host sample, best of 5 (bounded ~1 s)."""
+    def cpu_rate(self):
+        """oracle.memory.copy of a 256 MiB host sample."""
         import numpy as np
 
         from oracle import memory
 
         sample = np.random.default_rng(COPY_SEED).uniform(-1, 1, size=2**26).astype(np.float32)
-        memory.copy(sample)
-        best = None
-        for _ in range(5):
-            start = time.perf_counter()
-            memory.copy(sample)
-            elapsed = time.perf_counter() - start
-            best = elapsed if best is None else min(best, elapsed)
-        return {"value": 2 * sample.nbytes / best / 1e9, "unit": "GB/s",
-                "sample": "numpy copy (oracle.memory.copy) of 2^26 fp32 (256 MiB) on the host, best of 5"}
+        best = _best_of(lambda: memory.copy(sample), CPU_BUDGET_S / 4)
+        return 2 * sample.nbytes / best / 1e9, 1, "oracle.memory.copy (numpy) of 2^26 fp32 (256 MiB)"
 
 
-def build_workloads(torch, selected):
-    workloads = [CopyWorkload(torch)]
+class PeakWorkload:
+    """tensor_<dtype> row: resident-operand MFMA peak kernel."""
+
+    unit, bound = "TFLOP/s", "mfma"
+
+    def __init__(self, torch, dtype, blocks):
+        from triton_chip_benchmarks_amd import _native, bench_tensor
+
+        self.torch, self.bt, self.dtype = torch, bench_tensor, dtype
+        self.name = "peak_mxfp4" if dtype == "fp4" else f"peak_{dtype}"
+        self.metric_key = f"tensor_{dtype}"
+        m, n, k = PEAK_TILES[dtype]
+        self.config = next(c for c in _native.peak_configs(dtype)
+                           if (c["tile_m"], c["tile_n"], c["tile_k"]) == (m, n, k) and c["chains"] == 2
+                           and not c["b_nk"])
+        self.kernel = _native.peak_kernel_name(dtype, self.config)
+        self.blocks = blocks
+        if dtype == "fp4":
+            self.a, self.b, self.c, self.scales, self.values = bench_tensor.fp4_peak_inputs(blocks, self.config, "cuda")
+        else:
+            self.a, self.b, self.c, b_logical = bench_tensor.peak_inputs(blocks, self.config, dtype, "cuda")
+            self.scales, self.values = None, (self.a, b_logical)
+        self.work = 2 * m * n * k * PEAK_ITERATIONS * self.config["chains"] * blocks  # bench_tensor.py:1242
+        self.dtype_label = {"bf16": "bf16", "fp8": "fp8_e4m3", "fp4": "mxfp4_e2m1"}[dtype]
+        self.config_summary = {"tile": f"{m}x{n}x{k}", "chains": self.config["chains"], "blocks": blocks,
+                               "iterations": PEAK_ITERATIONS, "b_layout": "kn"}
+
+    def launch(self):
+        self.bt.launch_peak(self.dtype, self.config, self.a, self.b, self.c, PEAK_ITERATIONS, self.scales)
+
+    def validate(self):
+        self.c.fill_(float("nan"))
+        self.launch()
+        reference = self.bt.exact_reference(self.values[0], self.values[1], PEAK_ITERATIONS, self.torch.float32)
+        self.torch.cuda.synchronize()
+        result = self.bt.validate_peak(self.c, reference, self.dtype, self.config["tile_k"], PEAK_ITERATIONS)
+        return (f"every output within atol {result['atol']:.3g} of the exact float64 lattice reference "
+                f"(max error {result['max_abs_error']:.3g})")
+
+    def rate(self, ms):
+        return self.work / (ms * 1e9)  # TFLOP/s
+
+    def cpu_rate(self):
+        """The same tile products on the host: oracle.tensor.peak_reference over a block sample."""
+        import numpy as np
+
+        from oracle import tensor as ot
+
+        m, n, k = PEAK_TILES[self.dtype]
+        rng = np.random.default_rng(0)
+        blocks = 64
+        a = ot.ternary_lattice(rng, (blocks, m, k))
+        b = ot.ternary_lattice(rng, (2, blocks, k, n))
+        # One host iteration = both chains' tile products of every sampled block.
+        best = _best_of(lambda: ot.peak_reference(a, b, 1), CPU_BUDGET_S / 4)
+        flops = 2 * m * n * k * 2 * blocks
+        return flops / best / 1e12, _blas_threads(), (
+            f"oracle.tensor.peak_reference (numpy float64 matmul) of {blocks} blocks x 2 chains of "
+            f"{m}x{n}x{k} tiles, best repeat within {CPU_BUDGET_S / 4:g} s")
+
+
+def _blas_threads():
     try:
-        from triton_chip_benchmarks_amd import headline
+        from threadpoolctl import threadpool_info
+
+        return max((pool.get("num_threads", 1) for pool in threadpool_info()), default=1)
     except ImportError:
-        headline = None
-    if headline is not None:
-        workloads += headline.peak_workloads(torch)
+        return os.cpu_count() or 1
+
+
+def build_workloads(torch, selected, blocks):
+    workloads = [CopyWorkload(torch)] + [PeakWorkload(torch, d, blocks) for d in ("bf16", "fp8", "fp4")]
     if selected:
+        unknown = set(selected) - {w.name for w in workloads}
+        if unknown:
+            raise SystemExit(f"unknown rows: {', '.join(sorted(unknown))}")
         workloads = [w for w in workloads if w.name in selected]
     return workloads
 
@@ -139,9 +214,9 @@ def build_workloads(torch, selected):
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported. Every headline kernel "
-              "runs on a single GPU; a multi-GPU figure would be the sum of independent per-GPU rates, "
-              "which this build does not launch.", file=sys.stderr)
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported. Every headline kernel runs "
+              "on a single GPU, and a multi-GPU figure would be the sum of independent per-GPU rates, which "
+              "this build does not launch.", file=sys.stderr)
         return 2
     if args.steps <= 0 or args.warmup < 0:
         print("--steps must be positive and --warmup non-negative", file=sys.stderr)
@@ -153,7 +228,8 @@ def main(argv=None):
 
     require_gpu(0)
     info = _native.device_query(0)
-    workloads = build_workloads(torch, args.rows)
+    blocks = PEAK_BLOCKS_PER_CU * info["compute_units"]
+    workloads = build_workloads(torch, args.rows, blocks)
     checks = {w.name: w.validate() for w in workloads}
     for _ in range(args.warmup):
         for w in workloads:
@@ -161,8 +237,7 @@ def main(argv=None):
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(workloads) + 1)]
-              for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(workloads) + 1)] for _ in range(args.steps)]
     total_start, total_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     total_start.record(stream)
@@ -175,43 +250,48 @@ def main(argv=None):
     torch.cuda.synchronize()
     total_ms = total_start.elapsed_time(total_end)
 
-    traffic = _traffic_table()
+    traffic = traffic_table()
     rows = []
     for index, w in enumerate(workloads):
         durations = [events[s][index].elapsed_time(events[s][index + 1]) for s in range(args.steps)]
         average = sum(durations) / len(durations)
         achieved = w.rate(average)
-        peak, unit, basis = roofline.PEAKS[w.metric_key]
-        rows.append({"row": w.metric_key, "kernel": w.kernel, "value": achieved, "unit": w.unit,
-                     "ms_per_launch": average, "min_ms": min(durations), "peak": peak,
-                     "frac": achieved / peak, "peak_basis": basis, "bound": w.bound,
-                     "work_per_launch": w.work, "validation": checks[w.name],
-                     "traffic_bytes_per_launch": traffic.get(w.kernel)})
+        peak, _unit, basis = roofline.PEAKS[w.metric_key]
+        rows.append({"row": w.metric_key, "name": w.name, "kernel": w.kernel, "value": achieved, "unit": w.unit,
+                     "ms_per_launch": average, "best_ms": min(durations), "peak": peak, "frac": achieved / peak,
+                     "peak_basis": basis, "bound": w.bound, "algorithmic_work_per_launch": w.work,
+                     "work_unit": "bytes" if w.bound == "hbm" else "flop",
+                     "traffic_bytes_per_launch": traffic.get(w.kernel),
+                     "config": getattr(w, "config_summary", None) or w.config, "validation": checks[w.name]})
     value = 100.0 * sum(row["frac"] for row in rows) / len(rows)
     dominant = max(rows, key=lambda row: row["ms_per_launch"])
-    roofline_block = {
-        "bound": dominant["bound"], "kernel": dominant["kernel"],
-        "achieved": dominant["value"],
-        "peak": dominant["peak"], "unit": dominant["unit"], "frac": dominant["frac"],
-        "traffic": dominant["traffic_bytes_per_launch"],
-        "work_per_launch": dominant["work_per_launch"],
-    }
+    roofline_block = {"bound": dominant["bound"], "kernel": dominant["kernel"], "row": dominant["row"],
+                      "achieved": dominant["value"], "peak": dominant["peak"], "unit": dominant["unit"],
+                      "frac": dominant["frac"], "traffic": dominant["traffic_bytes_per_launch"],
+                      "algorithmic_work_per_launch": dominant["algorithmic_work_per_launch"],
+                      "ms_per_launch": dominant["ms_per_launch"]}
     cpu = None
     if not args.no_cpu_baseline:
-        baseline = workloads[0].cpu_baseline()
-        cores = 1  # numpy copy is single-threaded
-        cpu = {"value": baseline["value"], "unit": baseline["unit"], "cores": cores, "kind": "port",
-               "sample": baseline["sample"], "host_cpu_count": os.cpu_count(),
-               "gpu_over_cpu": rows[0]["value"] / baseline["value"] if rows[0]["unit"] == baseline["unit"] else None}
+        cpu_rows = []
+        for w in workloads:
+            cpu_value, cores, sample = w.cpu_rate()
+            peak = roofline.PEAKS[w.metric_key][0]
+            cpu_rows.append({"row": w.metric_key, "value": cpu_value, "unit": w.unit, "cores": cores,
+                             "sample": sample, "frac_of_mi355x_peak": cpu_value / peak})
+        cpu = {"value": 100.0 * sum(r["frac_of_mi355x_peak"] for r in cpu_rows) / len(cpu_rows),
+               "unit": "% of MI355X peak (mean over headline rows)",
+               "cores": max(r["cores"] for r in cpu_rows), "kind": "port",
+               "sample": "; ".join(f"{r['row']}: {r['sample']}" for r in cpu_rows),
+               "host_cpu_count": os.cpu_count(), "rows": cpu_rows}
     line = {
         "metric": METRIC, "value": value, "unit": "% of MI355X peak (mean over headline rows)",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": total_ms / args.steps, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": ",".join(sorted({w.dtype for w in workloads})),
-        "data": "synthetic (seeded uniform / exact-lattice operands, resident in HBM)",
-        "config": {"workload": " + ".join(w.name for w in workloads),
-                   "copy_elements": COPY_ELEMENTS, "device": info["name"], "arch": info["arch"],
-                   "compute_units": info["compute_units"]},
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": total_ms / args.steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": ",".join(getattr(w, "dtype_label", w.dtype) for w in workloads),
+        "data": "synthetic: seeded uniform fp32 copy source; exact-lattice MFMA operands, resident in HBM",
+        "config": {"workload": " + ".join(w.name for w in workloads), "device": info["name"], "arch": info["arch"],
+                   "compute_units": info["compute_units"], "peak_blocks": blocks,
+                   "peak_iterations": PEAK_ITERATIONS, "copy_elements": COPY_ELEMENTS},
         "roofline": roofline_block, "cpu_baseline": cpu, "rows": rows,
     }
     print(json.dumps(line))

@@ -105,6 +105,53 @@ int mb_copy(const void* src, void* dst, uint64_t bytes, uint32_t block_threads,
 int mb_read_sum(int dtype, const void* src, float* sink, uint64_t elements,
                 uint32_t block_elements, uint32_t block_threads, void* stream);
 
+/* ---- tensor: resident-operand matrix peak ------------------------------- */
+
+/* Matrix operand formats. */
+#define MB_MATRIX_BF16 0
+#define MB_MATRIX_F16 1
+#define MB_MATRIX_F32 2      /* IEEE fp32 operands, v_mfma_f32_32x32x2_f32 */
+#define MB_MATRIX_TF32 3     /* always MB_ERR_UNSUPPORTED: gfx950 has no xf32 MFMA */
+#define MB_MATRIX_I8 4       /* int8 operands, int32 accumulate */
+#define MB_MATRIX_F64 5      /* fp64 operands and accumulate */
+#define MB_MATRIX_FP8_E4M3 6 /* OCP FP8 E4M3 (fn) operands, fp32 accumulate */
+#define MB_MATRIX_MXFP4 7    /* OCP MX FP4: E2M1 two per byte + E8M0 scale per 32 K */
+
+typedef struct mb_peak_config {
+  uint32_t tile_m;  /* rows of A and C per workgroup */
+  uint32_t tile_n;  /* columns of B and C per workgroup */
+  uint32_t tile_k;  /* reduction length in elements (E2M1 elements for MXFP4) */
+  uint32_t chains;  /* independent accumulators, one B operand each */
+  uint32_t b_nk;    /* 0: B tile stored [K][N] (N contiguous); 1: [N][K] */
+  uint32_t mfma_m;  /* MFMA output rows (32 or 16) selecting the instruction; 0 = first match */
+  uint32_t threads; /* workgroup size (output only) */
+} mb_peak_config;
+
+/* Tile configurations compiled for `format`; writes up to `capacity` entries
+ * to `out` (which may be NULL) and returns how many exist. */
+int mb_tensor_peak_configs(int format, mb_peak_config* out, int capacity);
+
+/* Registered kernel name of a configuration (for the instruction audit), or
+ * NULL when no such kernel exists. */
+const char* mb_tensor_peak_kernel_name(int format, const mb_peak_config* config);
+
+/* Resident-operand peak: workgroup w computes, for each chain c,
+ *   C[c][w] = iterations * (A[w] . B[c][w])
+ * in the format's accumulator (fp32; int32 for I8; fp64 for F64), reading its
+ * operands from HBM once. Layouts (row-major, all contiguous):
+ *   A [blocks][tile_m][tile_k]            (MXFP4: [tile_k/2] bytes, low nibble = even k)
+ *   B [chains][blocks][tile_k][tile_n]    (b_nk: [chains][blocks][tile_n][tile_k];
+ *                                          MXFP4 [tile_k/2][tile_n] packed along K)
+ *   scale_a [blocks][tile_m][tile_k/32], scale_b [blocks][tile_n][tile_k/32] (MXFP4 only)
+ *   C [chains][blocks][tile_m][tile_n]
+ * Buffer sizes are checked against the configuration before launching.
+ * Replaces: bench_tensor.py:406-449 (_tensor_peak_kernel), 452-488
+ * (_tensor_peak_scaled_kernel) and 581-600 (_launch_peak). */
+int mb_tensor_peak(int format, const mb_peak_config* config, const void* a, uint64_t a_bytes,
+                   const void* b, uint64_t b_bytes, const void* scale_a, uint64_t scale_a_bytes,
+                   const void* scale_b, uint64_t scale_b_bytes, void* c, uint64_t c_bytes,
+                   uint32_t blocks, uint32_t iterations, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

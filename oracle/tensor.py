@@ -1,0 +1,157 @@
+"""Oracle for the tensor rows: exact-lattice references, tolerances, formats.
+
+Follows bench_tensor.py (reference):
+  E2M1 table and packing       55-69, 603-611
+  operand lattices             614-672
+  reference, tolerance, check  277-346
+  op count                     1242
+  FP32/FP64 precision probes   675-757
+FP8 E4M3FN and E8M0 decoding restate the OCP 8-bit floating point and OCP
+Microscaling v1.0 specifications bit by bit (no lookup into torch), so tests
+can pin them against torch's float8_e4m3fn conversion independently.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+E2M1_VALUES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                        -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float64)
+
+
+def e2m1_decode(codes: np.ndarray) -> np.ndarray:
+    """Value of each 4-bit E2M1 code: sign bit 3, exponent bits 2-1 (bias 1), mantissa bit 0."""
+    codes = np.asarray(codes, dtype=np.int64) & 15
+    sign = np.where(codes & 8, -1.0, 1.0)
+    exponent = (codes >> 1) & 3
+    mantissa = codes & 1
+    magnitude = np.where(exponent == 0, 0.5 * mantissa, (1.0 + 0.5 * mantissa) * 2.0 ** (exponent - 1))
+    return sign * magnitude
+
+
+def pack_e2m1(codes: np.ndarray) -> np.ndarray:
+    """Two codes per byte along the last axis, element 2i in the low nibble (bench_tensor.py:603-611)."""
+    codes = np.asarray(codes, dtype=np.uint8)
+    return ((codes[..., 1::2] & 15) << 4 | (codes[..., 0::2] & 15)).astype(np.uint8)
+
+
+def unpack_e2m1(packed: np.ndarray) -> np.ndarray:
+    packed = np.asarray(packed, dtype=np.uint8)
+    out = np.empty(packed.shape[:-1] + (packed.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = packed & 15
+    out[..., 1::2] = packed >> 4
+    return out
+
+
+def e8m0_decode(codes: np.ndarray) -> np.ndarray:
+    """2**(code-127); code 255 is NaN (OCP MX v1.0 scale format)."""
+    codes = np.asarray(codes, dtype=np.int64)
+    return np.where(codes == 255, np.nan, np.ldexp(1.0, codes - 127))
+
+
+def fp8_e4m3fn_decode(bits: np.ndarray) -> np.ndarray:
+    """E4M3FN: bias 7, subnormals, no infinities, S.1111.111 is NaN."""
+    bits = np.asarray(bits, dtype=np.int64) & 255
+    sign = np.where(bits & 128, -1.0, 1.0)
+    exponent = (bits >> 3) & 15
+    mantissa = bits & 7
+    value = np.where(exponent == 0, np.ldexp(mantissa / 8.0, -6),
+                     np.ldexp(1.0 + mantissa / 8.0, exponent - 7))
+    value = np.where((exponent == 15) & (mantissa == 7), np.nan, value)
+    return sign * value
+
+
+def fp8_e4m3fn_encode_exact(values: np.ndarray) -> np.ndarray:
+    """Bit pattern of values that E4M3FN represents exactly (raises otherwise)."""
+    table = fp8_e4m3fn_decode(np.arange(256))
+    values = np.asarray(values, dtype=np.float64)
+    out = np.empty(values.shape, dtype=np.uint8)
+    lookup = {}
+    for code in range(256):
+        if not np.isnan(table[code]) and (table[code] not in lookup or code < 128):
+            lookup.setdefault(float(table[code]), code)
+    for index, value in np.ndenumerate(values):
+        if float(value) not in lookup:
+            raise ValueError(f"{value} is not exactly representable in E4M3FN")
+        out[index] = lookup[float(value)]
+    return out
+
+
+def bf16_bits(values: np.ndarray) -> np.ndarray:
+    """bfloat16 bit patterns of values exactly representable in bfloat16."""
+    as32 = np.asarray(values, dtype=np.float32).view(np.uint32)
+    if np.any(as32 & 0xFFFF):
+        raise ValueError("values are not exactly representable in bfloat16")
+    return (as32 >> 16).astype(np.uint16)
+
+
+def peak_operation_count(m: int, n: int, k: int, iterations: int, chains: int, blocks: int) -> int:
+    """2*M*N*K*ITER*chains*blocks (bench_tensor.py:1242)."""
+    return 2 * m * n * k * iterations * chains * blocks
+
+
+def peak_tolerance(dtype: str, block_k: int, iterations: int) -> float:
+    """atol of the resident-peak check, rtol 0 (bench_tensor.py:302-325)."""
+    if dtype == "int8":
+        return 0.0
+    if dtype == "fp4":
+        return 4.0 * iterations * block_k * 2.0 ** -24
+    unit_roundoff = 2.0 ** -53 if dtype == "fp64" else 2.0 ** -24
+    return 4.0 * iterations * block_k / 256.0 * unit_roundoff
+
+
+def peak_reference(a: np.ndarray, b: np.ndarray, iterations: int) -> np.ndarray:
+    """C[c, w] = iterations * A[w] @ B[c, w] in float64 (bench_tensor.py:1220-1232).
+
+    a: [blocks, M, K] values; b: [chains, blocks, K, N] values.
+    """
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return np.stack([np.matmul(a, b[c]) for c in range(b.shape[0])]) * iterations
+
+
+def check_peak(actual: np.ndarray, reference: np.ndarray, dtype: str, block_k: int, iterations: int) -> float:
+    """Max abs error; raises past peak_tolerance (NaN fails)."""
+    error = np.abs(np.asarray(actual, dtype=np.float64) - reference)
+    tolerance = peak_tolerance(dtype, block_k, iterations)
+    if not np.all(error <= tolerance):
+        raise AssertionError(f"peak output differs: max_abs_error={np.nanmax(error):.6g} > atol {tolerance:.6g}")
+    return float(error.max()) if error.size else 0.0
+
+
+def ternary_lattice(rng: np.random.Generator, shape, scale: float = 1 / 16) -> np.ndarray:
+    """Random {-1, 0, 1} * scale operands (bench_tensor.py:664-666)."""
+    return rng.integers(-1, 2, size=shape).astype(np.float64) * scale
+
+
+def one_hot_rows(rng: np.random.Generator, shape, value: float = 1 / 16) -> np.ndarray:
+    """FP8 A operand: one `value` per row at a random K (bench_tensor.py:651-658)."""
+    out = np.zeros(shape, dtype=np.float64)
+    hot = rng.integers(0, shape[-1], size=shape[:-1])
+    np.put_along_axis(out, hot[..., None], value, axis=-1)
+    return out
+
+
+def fp32_precision_probe() -> tuple[np.ndarray, np.ndarray]:
+    """A (1+2^-12, 1+2^-9, 2^20) and B = I, 32x32 (bench_tensor.py:678-687)."""
+    a = np.full((32, 32), 1.0 + 2.0 ** -12)
+    a[0, 1], a[0, 2] = 1.0 + 2.0 ** -9, 2.0 ** 20
+    return a, np.eye(32)
+
+
+def fp64_precision_probe() -> tuple[np.ndarray, np.ndarray]:
+    """A with 1+2^-40 and a per-row marker, B = eye(16, 32) (bench_tensor.py:728-735)."""
+    a = np.full((32, 16), 1.0 + 2.0 ** -40)
+    a[:, 0] = np.arange(1, 33)
+    return a, np.eye(16, 32)
+
+
+def gemm_reference(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """C = A @ B in float64 (bench_tensor.py:277-286); exact on the BASELINE lattices."""
+    return np.matmul(np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64))
+
+
+def gemm_relative_error(actual: np.ndarray, reference: np.ndarray) -> float:
+    """max |C - R| / max |R|, the normwise error used for the BF16/FP16/FP64 GEMM rows."""
+    scale = float(np.max(np.abs(reference))) or 1.0
+    return float(np.max(np.abs(np.asarray(actual, dtype=np.float64) - reference))) / scale

@@ -68,3 +68,36 @@ def test_invalid_arguments_are_rejected_before_any_launch():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_native.NativeLibraryMissing):
         _native.load(tmp_path / "absent.so")
+
+
+def test_tensor_peak_tables_and_host_side_rejections():
+    """Config enumeration and argument checks run on the host, before any launch."""
+    import ctypes
+
+    library = _native.load()
+    for dtype in ("bf16", "fp16", "fp32", "int8", "fp64", "fp8", "fp4"):
+        configs = _native.peak_configs(dtype)
+        assert configs, dtype
+        assert {c["b_nk"] for c in configs} == {0, 1}
+        for config in configs:
+            name = _native.peak_kernel_name(dtype, config)
+            assert name and name in _native.kernel_names()
+    tf32 = _native.MATRIX_FORMATS["tf32"]
+    assert library.mb_tensor_peak_configs(tf32, None, 0) == _native.MB_ERR_UNSUPPORTED
+    assert "xf32" in _native.last_error()
+    config = _native.peak_config(_native.peak_configs("bf16")[0])
+    bad = _native.peak_config({"tile_m": 48, "tile_n": 48, "tile_k": 48, "chains": 2})
+    fake = 1 << 20  # never dereferenced: every call below fails its host-side checks
+    assert library.mb_tensor_peak(tf32, ctypes.byref(config), fake, 1 << 30, fake, 1 << 30, None, 0, None, 0,
+                                  fake, 1 << 30, 1, 1, None) == _native.MB_ERR_UNSUPPORTED
+    assert library.mb_tensor_peak(0, ctypes.byref(bad), fake, 1 << 30, fake, 1 << 30, None, 0, None, 0,
+                                  fake, 1 << 30, 1, 1, None) == _native.MB_ERR_INVALID
+    assert library.mb_tensor_peak(0, ctypes.byref(config), fake, 16, fake, 1 << 30, None, 0, None, 0,
+                                  fake, 1 << 30, 1, 1, None) == _native.MB_ERR_INVALID
+    assert "too small" in _native.last_error()
+    assert library.mb_tensor_peak(0, ctypes.byref(config), fake, 1 << 30, fake, 1 << 30, None, 0, None, 0,
+                                  fake, 1 << 30, 1, 0, None) == _native.MB_ERR_INVALID
+    fp4 = _native.peak_config(_native.peak_configs("fp4")[0])
+    assert library.mb_tensor_peak(7, ctypes.byref(fp4), fake, 1 << 30, fake, 1 << 30, None, 0, None, 0,
+                                  fake, 1 << 30, 1, 1, None) == _native.MB_ERR_INVALID
+    assert "scales" in _native.last_error()

@@ -61,6 +61,18 @@ class KernelAttributes(ctypes.Structure):
                 ("lds_bytes", ctypes.c_int64), ("scratch_bytes", ctypes.c_int64)]
 
 
+class PeakConfig(ctypes.Structure):
+    _fields_ = [("tile_m", ctypes.c_uint32), ("tile_n", ctypes.c_uint32), ("tile_k", ctypes.c_uint32),
+                ("chains", ctypes.c_uint32), ("b_nk", ctypes.c_uint32), ("mfma_m", ctypes.c_uint32),
+                ("threads", ctypes.c_uint32)]
+
+    def as_dict(self) -> dict:
+        return {field: getattr(self, field) for field, _ in self._fields_}
+
+
+# Matrix formats of the tensor entry points (MB_MATRIX_*).
+MATRIX_FORMATS = {"bf16": 0, "fp16": 1, "fp32": 2, "tf32": 3, "int8": 4, "fp64": 5, "fp8": 6, "fp4": 7}
+
 _u64, _u32, _i32, _ptr = ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p
 
 # name -> (restype, argtypes). Every symbol here is declared in
@@ -74,6 +86,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mb_kernel_attributes_query": (_i32, [ctypes.c_char_p, ctypes.POINTER(KernelAttributes)]),
     "mb_copy": (_i32, [_ptr, _ptr, _u64, _u32, _u32, _u32, _u32, _ptr]),
     "mb_read_sum": (_i32, [_i32, _ptr, _ptr, _u64, _u32, _u32, _ptr]),
+    "mb_tensor_peak_configs": (_i32, [_i32, ctypes.POINTER(PeakConfig), _i32]),
+    "mb_tensor_peak_kernel_name": (ctypes.c_char_p, [_i32, ctypes.POINTER(PeakConfig)]),
+    "mb_tensor_peak": (_i32, [_i32, ctypes.POINTER(PeakConfig), _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64,
+                              _ptr, _u64, _u32, _u32, _ptr]),
 }
 
 _lock = threading.Lock()
@@ -146,6 +162,47 @@ def kernel_attributes(name: str) -> dict:
     attributes = KernelAttributes()
     call("mb_kernel_attributes_query", name.encode(), ctypes.byref(attributes))
     return {field: getattr(attributes, field) for field, _ in KernelAttributes._fields_}
+
+
+def peak_configs(dtype: str) -> list[dict]:
+    """Compiled resident-peak tiles of a matrix format."""
+    library = load()
+    code = MATRIX_FORMATS[dtype]
+    count = library.mb_tensor_peak_configs(code, None, 0)
+    if count < 0:
+        check(count)
+    configs = (PeakConfig * max(count, 1))()
+    library.mb_tensor_peak_configs(code, configs, count)
+    return [configs[index].as_dict() for index in range(count)]
+
+
+def peak_config(config: dict) -> PeakConfig:
+    return PeakConfig(config["tile_m"], config["tile_n"], config["tile_k"], config["chains"],
+                      int(config.get("b_nk", 0)), int(config.get("mfma_m", 0)), int(config.get("threads", 0)))
+
+
+def peak_kernel_name(dtype: str, config: dict) -> str | None:
+    name = load().mb_tensor_peak_kernel_name(MATRIX_FORMATS[dtype], ctypes.byref(peak_config(config)))
+    return name.decode() if name else None
+
+
+def _buffer(tensor):
+    if tensor is None:
+        return None, 0
+    return tensor.data_ptr(), tensor.numel() * tensor.element_size()
+
+
+def tensor_peak(dtype: str, config: dict, a, b, c, blocks: int, iterations: int, scale_a=None, scale_b=None,
+                stream=None) -> None:
+    """One launch of the resident-operand peak kernel on the current stream."""
+    a_ptr, a_bytes = _buffer(a)
+    b_ptr, b_bytes = _buffer(b)
+    sa_ptr, sa_bytes = _buffer(scale_a)
+    sb_ptr, sb_bytes = _buffer(scale_b)
+    c_ptr, c_bytes = _buffer(c)
+    call("mb_tensor_peak", MATRIX_FORMATS[dtype], ctypes.byref(peak_config(config)), a_ptr, a_bytes, b_ptr,
+         b_bytes, sa_ptr, sa_bytes, sb_ptr, sb_bytes, c_ptr, c_bytes, blocks, iterations,
+         stream_handle(stream))
 
 
 def stream_handle(stream=None) -> int | None:

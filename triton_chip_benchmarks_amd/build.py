@@ -5,8 +5,8 @@ Outputs, all inside the package directory:
   _build/<unit>.o                 per-translation-unit objects
   _build/<unit>.gfx950.s          device assembly with the AMDHSA metadata
                                   (VGPR/AGPR/SGPR counts, LDS, scratch, spills)
-  _build/libmi355x_bench.gfx950.co   the gfx950 code object embedded in the .so
-  _build/libmi355x_bench.gfx950.isa  llvm-objdump disassembly of that object
+  _build/<unit>.gfx950.co         each object's gfx950 code object (embedded in the .so)
+  _build/libmi355x_bench.gfx950.isa  llvm-objdump disassembly of all of them
 
 The instruction audit reads the disassembly of the code object that the
 library actually launches, so the audited instructions are the executed ones.
@@ -27,7 +27,6 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = PACKAGE.parent / "include"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libmi355x_bench.so"
-CODE_OBJECT = BUILD / "libmi355x_bench.gfx950.co"
 DISASSEMBLY = BUILD / "libmi355x_bench.gfx950.isa"
 ARCH = "gfx950"
 
@@ -71,21 +70,35 @@ def _compile(source: Path) -> Path:
     return obj
 
 
-def _extract_code_object() -> None:
-    """Unbundle the gfx950 code object from the library's HIP fat binary."""
-    fatbin = BUILD / "libmi355x_bench.hip_fatbin"
-    _run([str(LLVM_BIN / "llvm-objcopy"), "--dump-section", f".hip_fatbin={fatbin}", str(LIBRARY),
-          str(BUILD / "objcopy.discard")], "extract .hip_fatbin")
-    (BUILD / "objcopy.discard").unlink(missing_ok=True)
-    _run([str(LLVM_BIN / "clang-offload-bundler"), "--unbundle", "--type=o",
-          f"--targets=hipv4-amdgcn-amd-amdhsa--{ARCH}", f"--input={fatbin}",
-          f"--output={CODE_OBJECT}"], "unbundle gfx950 code object")
-    completed = subprocess.run([str(LLVM_BIN / "llvm-objdump"), "-d", f"--mcpu={ARCH}",
-                                "--no-show-raw-insn", str(CODE_OBJECT)],
-                               capture_output=True, text=True)
-    if completed.returncode:
-        raise RuntimeError(f"llvm-objdump failed:\n{completed.stderr}")
-    DISASSEMBLY.write_text(completed.stdout)
+def _extract_code_objects(objects: list[Path]) -> None:
+    """Unbundle each object's gfx950 code object and disassemble all of them.
+
+    Every object file carries its own HIP fat binary, and the linked library
+    embeds them side by side, so the per-object code objects are exactly the
+    device code the library launches.
+    """
+    listings = []
+    for obj in objects:
+        fatbin = BUILD / f"{obj.stem}.hip_fatbin"
+        code_object = BUILD / f"{obj.stem}.{ARCH}.co"
+        dumped = subprocess.run([str(LLVM_BIN / "llvm-objcopy"), "--dump-section", f".hip_fatbin={fatbin}",
+                                 str(obj), str(BUILD / "objcopy.discard")], capture_output=True, text=True)
+        (BUILD / "objcopy.discard").unlink(missing_ok=True)
+        if dumped.returncode and "not found" in dumped.stderr:
+            continue  # a host-only translation unit has no device code
+        if dumped.returncode:
+            raise RuntimeError(f"extract the fat binary of {obj.name} failed:\n{dumped.stderr}")
+        _run([str(LLVM_BIN / "clang-offload-bundler"), "--unbundle", "--type=o",
+              f"--targets=hipv4-amdgcn-amd-amdhsa--{ARCH}", f"--input={fatbin}",
+              f"--output={code_object}"], f"unbundle {obj.name}")
+        fatbin.unlink()
+        completed = subprocess.run([str(LLVM_BIN / "llvm-objdump"), "-d", f"--mcpu={ARCH}",
+                                    "--no-show-raw-insn", str(code_object)],
+                                   capture_output=True, text=True)
+        if completed.returncode:
+            raise RuntimeError(f"llvm-objdump failed on {code_object}:\n{completed.stderr}")
+        listings.append(completed.stdout)
+    DISASSEMBLY.write_text("\n".join(listings))
 
 
 def build(verbose: bool = True) -> Path:
@@ -101,7 +114,7 @@ def build(verbose: bool = True) -> Path:
     _run([_hipcc(), "-shared", f"--offload-arch={ARCH}", *objects_as_str(objects), "-o", str(temporary)],
          "link libmi355x_bench.so")
     temporary.replace(LIBRARY)
-    _extract_code_object()
+    _extract_code_objects(objects)
     if verbose:
         print(f"built {LIBRARY.relative_to(PACKAGE.parent)} from {len(units)} sources "
               f"({', '.join(unit.name for unit in units)})")

@@ -45,6 +45,9 @@ struct KernelEntry {
 };
 void register_kernel(const char* name, const void* func);
 
+// MB_OK for a matrix format with kernels; MB_ERR_UNSUPPORTED for TF32.
+int matrix_format_check(int format, const char* entry);
+
 struct KernelRegistrar {
   KernelRegistrar(const char* name, const void* func) { register_kernel(name, func); }
 };

@@ -1,0 +1,150 @@
+// gfx950 matrix-core (MFMA) instruction traits shared by the resident-peak and
+// GEMM kernels.
+//
+// Every trait describes one v_mfma instruction as a wave64 operation on an
+// M x N output tile with K reduction elements:
+//   * operand fragments: lane l holds LANE_BYTES contiguous bytes of K for
+//     row/column (l % M) of A/B, at K byte offset (l / M) * LANE_BYTES within
+//     the instruction's K_BYTES = (64 / M) * LANE_BYTES;
+//   * accumulator: ACC_REGS values per lane; out_row/out_col give the output
+//     element each accumulator register of each lane holds.
+// Storage sizes are in bytes so packed formats (two E2M1 codes per byte) use
+// the same tile arithmetic as byte-sized ones.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mb {
+
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Output position of accumulator register r in lane l for a 32x32 tile
+// (four row quads per register group of four) and a 16x16 tile.
+__device__ __forceinline__ int out_row_32(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+__device__ __forceinline__ int out_row_16(int lane, int r) { return 4 * (lane >> 4) + r; }
+
+// v_mfma_f32_32x32x16_bf16: 8 bf16 per lane, fp32 accumulate.
+struct MfmaBf16 {
+  static constexpr int M = 32, N = 32, K = 16, ELEM_BITS = 16, LANE_BYTES = 16, ACC_REGS = 16;
+  static constexpr bool SCALED = false;
+  using Frag = i32x4;
+  using Acc = f32x16;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_f32_32x32x16_f16: 8 fp16 per lane, fp32 accumulate.
+struct MfmaF16 {
+  static constexpr int M = 32, N = 32, K = 16, ELEM_BITS = 16, LANE_BYTES = 16, ACC_REGS = 16;
+  static constexpr bool SCALED = false;
+  using Frag = i32x4;
+  using Acc = f32x16;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_i32_32x32x32_i8: 16 int8 per lane, int32 accumulate.
+struct MfmaI8 {
+  static constexpr int M = 32, N = 32, K = 32, ELEM_BITS = 8, LANE_BYTES = 16, ACC_REGS = 16;
+  static constexpr bool SCALED = false;
+  using Frag = i32x4;
+  using Acc = i32x16;
+  using Out = int32_t;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_f32_32x32x64_f8f6f4 with both formats FP8 E4M3 (cbsz = blgp = 0):
+// 32 fp8 per lane, fp32 accumulate, no block scales. The scaled builtin with
+// zero scale operands selects the unscaled instruction.
+struct MfmaFp8 {
+  static constexpr int M = 32, N = 32, K = 64, ELEM_BITS = 8, LANE_BYTES = 32, ACC_REGS = 16;
+  static constexpr bool SCALED = false;
+  using Frag = i32x8;
+  using Acc = f32x16;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_scale_f32_32x32x64_f8f6f4 with both formats FP4 E2M1 (cbsz = blgp =
+// 4): 32 E2M1 codes (16 bytes, low nibble first) per lane; each lane also
+// supplies the E8M0 scale of its 32-element K group (byte 0 of a VGPR).
+struct MfmaMxfp4 {
+  static constexpr int M = 32, N = 32, K = 64, ELEM_BITS = 4, LANE_BYTES = 16, ACC_REGS = 16;
+  static constexpr bool SCALED = true;
+  using Frag = i32x4;
+  using Acc = f32x16;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int scale_a, int scale_b) {
+    const i32x8 wa = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+    const i32x8 wb = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, wb, c, 4, 4, 0, scale_a, 0, scale_b);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_f32_32x32x2_f32: one fp32 per lane, IEEE fp32 multiply-accumulate.
+struct MfmaF32 {
+  static constexpr int M = 32, N = 32, K = 2, ELEM_BITS = 32, LANE_BYTES = 4, ACC_REGS = 16;
+  static constexpr bool SCALED = false;
+  using Frag = float;
+  using Acc = f32x16;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_f64_16x16x4_f64: one fp64 per lane, fp64 accumulate (16x16 tile).
+struct MfmaF64 {
+  static constexpr int M = 16, N = 16, K = 4, ELEM_BITS = 64, LANE_BYTES = 8, ACC_REGS = 4;
+  static constexpr bool SCALED = false;
+  using Frag = double;
+  using Acc = f64x4;
+  using Out = double;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  // The four fp64 results of a lane are strided by 4 rows (measured on gfx950
+  // with a row/column-marked product), unlike the 16x16 fp32 forms.
+  __device__ static __forceinline__ int out_row(int lane, int r) { return (lane >> 4) + 4 * r; }
+};
+
+template <class Op>
+struct MfmaGeometry {
+  static constexpr int LANE_GROUPS = 64 / Op::M;                     // lanes sharing a row, split over K
+  static constexpr int K_BYTES = LANE_GROUPS * Op::LANE_BYTES;       // K bytes per instruction
+  static constexpr int FLOPS = 2 * Op::M * Op::N * Op::K;            // multiply + add per instruction
+};
+
+// Load a fragment of Frag's size from 4-byte-aligned memory (LDS or global).
+template <class Frag>
+__device__ __forceinline__ Frag load_frag(const uint8_t* ptr) {
+  return *reinterpret_cast<const Frag*>(ptr);
+}
+
+}  // namespace mb

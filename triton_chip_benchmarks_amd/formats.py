@@ -1,0 +1,44 @@
+"""Operand formats of the matrix rows: OCP MX FP4 (E2M1 + E8M0) and FP8 E4M3.
+
+Host-side data preparation only: building packed operands for the kernels.
+The constants are fixed by the OCP Microscaling Formats v1.0 specification,
+as the reference states (bench_tensor.py:55-69).
+"""
+
+from __future__ import annotations
+
+FP4_PACKING_FACTOR = 2   # E2M1 elements per uint8 container
+MX_GROUP_SIZE = 32       # elements along K sharing one E8M0 scale
+E8M0_UNIT_SCALE = 127    # biased exponent of 2**0
+E8M0_BIAS = 127
+
+# The sixteen E2M1 values in code order: sign, two exponent bits, one mantissa bit.
+E2M1_MAGNITUDES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+E2M1_VALUES = E2M1_MAGNITUDES + tuple(-value for value in E2M1_MAGNITUDES)
+
+
+def pack_e2m1_pairs(codes):
+    """Pack E2M1 codes two per byte along the last axis; even k in the low nibble."""
+    import torch
+
+    if codes.shape[-1] % 2:
+        raise ValueError("E2M1 packing needs an even number of elements along the packed axis")
+    low = codes[..., 0::2].to(torch.int16)
+    high = codes[..., 1::2].to(torch.int16)
+    return ((high << 4) | (low & 15)).to(torch.uint8)
+
+
+def e2m1_decode(codes):
+    """Float64 values of E2M1 codes (any integer tensor of 0..15)."""
+    import torch
+
+    table = torch.tensor(E2M1_VALUES, dtype=torch.float64, device=codes.device)
+    return table[codes.long()]
+
+
+def e8m0_decode(codes):
+    """2**(code - 127) for E8M0 scale codes (255 is NaN in OCP MX)."""
+    import torch
+
+    values = torch.pow(2.0, codes.double() - E8M0_BIAS)
+    return torch.where(codes == 255, torch.full_like(values, float("nan")), values)
