@@ -152,6 +152,37 @@ int mb_tensor_peak(int format, const mb_peak_config* config, const void* a, uint
                    const void* scale_b, uint64_t scale_b_bytes, void* c, uint64_t c_bytes,
                    uint32_t blocks, uint32_t iterations, void* stream);
 
+/* ---- vector: register-resident arithmetic chains ------------------------ */
+
+/* Vector chain kinds. Storage of input/output/coefficients per kind:
+ *   F32 float, F64 double, F16 _Float16, BF16_* bfloat16 bits (uint16),
+ *   I8_DOT4 int32 (four packed signed bytes of state; weights packed the same). */
+#define MB_VECTOR_F32 0       /* x <- fma(x, a, b_c), v_fma_f32 */
+#define MB_VECTOR_F16 1       /* x <- fma(x, a, b_c), v_pk_fma_f16 (two chains per VGPR) */
+#define MB_VECTOR_BF16_DOT2 2 /* x <- bf16(a*x + b_c), v_dot2_f32_bf16 + v_cvt_pk_bf16_f32 */
+#define MB_VECTOR_F64 3       /* x <- fma(x, a, b_c), v_fma_f64 */
+#define MB_VECTOR_I8_DOT4 4   /* x <- dot4(bytes(x), bytes(W)) + b_c, v_dot4_i32_i8 */
+#define MB_VECTOR_BF16_FMA 5  /* x <- bf16(fma(f32(x), a, b_c)), v_fma_f32 + v_cvt_pk_bf16_f32 */
+#define MB_VECTOR_FP8 6       /* always MB_ERR_UNSUPPORTED: no FP8 vector arithmetic on gfx950 */
+#define MB_VECTOR_FP4 7       /* always MB_ERR_UNSUPPORTED: no FP4 vector arithmetic on gfx950 */
+
+/* Registered kernel name of (kind, unroll), or NULL. */
+const char* mb_vector_kernel_name(int kind, uint32_t unroll);
+
+/* Eight independent chains per element: for c in 0..7 and every element i,
+ *   Output[c][i] = update^iterations(Input[c][i]) with a = Coefficients[0] (for
+ *   I8_DOT4 the packed weights W) and b_c = Coefficients[1 + c].
+ * One thread per element: `elements` is a positive multiple of
+ * `block_threads` (a multiple of 64 up to 1024); the loop body applies
+ * `unroll` (1, 4, 8 or 16) updates per trip and `iterations` must be a
+ * multiple of it. Buffer sizes are checked before launching.
+ * Replaces: bench_vector.py:182-319 (vector_fma_kernel, with _float_update,
+ * _widened_fma_update and _dp4a_update) and 1032-1051 (launch_vector). */
+int mb_vector_chains(int kind, const void* input, void* output, const void* coefficients,
+                     uint64_t elements, uint32_t iterations, uint32_t unroll, uint32_t block_threads,
+                     uint64_t input_bytes, uint64_t output_bytes, uint64_t coefficient_bytes,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,3 +101,23 @@ def test_tensor_peak_tables_and_host_side_rejections():
     assert library.mb_tensor_peak(7, ctypes.byref(fp4), fake, 1 << 30, fake, 1 << 30, None, 0, None, 0,
                                   fake, 1 << 30, 1, 1, None) == _native.MB_ERR_INVALID
     assert "scales" in _native.last_error()
+
+
+def test_vector_kernels_and_host_side_rejections():
+    library = _native.load()
+    for kind in (0, 1, 2, 3, 4, 5):
+        for unroll in (1, 4, 8, 16):
+            name = library.mb_vector_kernel_name(kind, unroll)
+            assert name and name.decode() in _native.kernel_names()
+    assert library.mb_vector_kernel_name(0, 3) is None
+    fake = 1 << 20  # never dereferenced: every call below fails its host-side checks
+    for kind in (6, 7):  # FP8 / FP4 have no VALU arithmetic on gfx950
+        assert library.mb_vector_chains(kind, fake, fake, fake, 64, 1, 1, 64, 1 << 20, 1 << 20, 64,
+                                        None) == _native.MB_ERR_UNSUPPORTED
+    assert library.mb_vector_chains(0, fake, fake, fake, 100, 4, 1, 64, 1 << 20, 1 << 20, 64,
+                                    None) == _native.MB_ERR_INVALID  # elements not a multiple of 64
+    assert library.mb_vector_chains(0, fake, fake, fake, 64, 6, 4, 64, 1 << 20, 1 << 20, 64,
+                                    None) == _native.MB_ERR_INVALID  # iterations not a multiple of unroll
+    assert library.mb_vector_chains(0, fake, fake, fake, 64, 4, 4, 64, 16, 1 << 20, 64,
+                                    None) == _native.MB_ERR_INVALID  # input too small
+    assert "too small" in _native.last_error()

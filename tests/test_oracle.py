@@ -1,0 +1,265 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Each oracle function is checked against something a plausible mistake would
+fail: the reference's published numbers (tests/golden/reference_published.json,
+extracted from its result files), its tests' known answers, brute force with
+exact rational arithmetic, closed forms, and torch's own format conversions.
+"""
+
+from fractions import Fraction
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import memory, tensor as ot, vector as ov
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_published.json").read_text())
+
+
+# ---- exact rational rounding, the brute-force checker ------------------------------------------
+
+def round_fraction(value: Fraction, precision: int, emin: int) -> Fraction:
+    """Round-to-nearest-even of an exact rational to a binary format (no overflow handling)."""
+    if value == 0:
+        return Fraction(0)
+    sign = -1 if value < 0 else 1
+    magnitude = abs(value)
+    exponent = magnitude.numerator.bit_length() - magnitude.denominator.bit_length()
+    if Fraction(2) ** exponent > magnitude:
+        exponent -= 1
+    exponent = max(exponent, emin)
+    quantum = Fraction(2) ** (exponent - (precision - 1))
+    scaled = magnitude / quantum
+    floor = scaled.numerator // scaled.denominator
+    remainder = scaled - floor
+    if remainder > Fraction(1, 2) or (remainder == Fraction(1, 2) and floor % 2 == 1):
+        floor += 1
+    return sign * floor * quantum
+
+
+F32 = (24, -126)
+F16 = (11, -14)
+BF16 = (8, -126)
+
+
+# ---- vector oracle ----------------------------------------------------------------------------
+
+def test_fp32_chain_matches_exact_rounding_step_by_step():
+    rng = np.random.default_rng(0)
+    x = rng.uniform(0.125, 1.0, 64).astype(np.float32).astype(np.float64)
+    a, b = float(np.float32(1 - 2.0**-14)), float(np.float32(3 * 2.0**-16))
+    inputs = np.tile(x, (8, 1))
+    coefficients = np.array([a] + [b] * 8)
+    emulated = ov.run_chains("fp32", inputs, coefficients, 7)[0]
+    for lane in range(64):
+        value = Fraction(x[lane])
+        for _ in range(7):
+            value = round_fraction(value * Fraction(a) + Fraction(b), *F32)
+        assert emulated[lane] == float(value)
+
+
+@pytest.mark.parametrize("dtype,fmt", [("fp16", F16), ("bf16", BF16)])
+@pytest.mark.parametrize("widened", [False, True])
+def test_narrow_chain_matches_exact_rounding(dtype, fmt, widened):
+    rng = np.random.default_rng(1)
+    x = ov.round_narrow(rng.uniform(-3, 3, 200), dtype)
+    a = float(ov.round_narrow(np.array([0.7071]), dtype)[0])
+    b = float(ov.round_narrow(np.array([0.01]), dtype)[0])
+    got = ov.run_chains(dtype, np.tile(x, (8, 1)), np.array([a] + [b] * 8), 5, widened=widened)[3]
+    for lane in range(200):
+        value = Fraction(x[lane])
+        for _ in range(5):
+            exact = value * Fraction(a) + Fraction(b)
+            value = round_fraction(round_fraction(exact, *F32), *fmt) if widened else round_fraction(exact, *fmt)
+        assert got[lane] == float(value), (lane, got[lane], float(value))
+
+
+def test_widened_and_single_rounding_differ_somewhere():
+    """The two narrow semantics are distinguishable, so tests choosing one mean something."""
+    rng = np.random.default_rng(2)
+    x = ov.round_narrow(rng.uniform(0.5, 1.0, 20000), "bf16")
+    a = ov.round_narrow(rng.uniform(0.5, 1.0, 20000), "bf16")
+    # A tiny addend puts the exact sum just off a product that sits on a bf16
+    # midpoint; rounding through fp32 first lands on the midpoint and ties to even.
+    b = ov.round_narrow(rng.uniform(2.0**-30, 2.0**-28, 20000), "bf16")
+    differ = 0
+    for i in range(20000):
+        single = ov.run_chains("bf16", np.full((1, 1), x[i]), np.array([a[i], b[i]]), 1, widened=False)[0, 0]
+        widened = ov.run_chains("bf16", np.full((1, 1), x[i]), np.array([a[i], b[i]]), 1, widened=True)[0, 0]
+        differ += single != widened
+        if differ:
+            break
+    assert differ
+
+
+def test_round_narrow_matches_torch_and_numpy_conversions():
+    import torch
+
+    rng = np.random.default_rng(3)
+    values = np.concatenate([rng.standard_normal(5000) * 10.0 ** rng.integers(-8, 5, 5000),
+                             [0.0, -0.0, 1e-8, 6.0e-8, 65504.0, 65519.0, 2.0**-24, 3 * 2.0**-26]])
+    assert np.array_equal(ov.round_narrow(values, "fp16"), values.astype(np.float16).astype(np.float64))
+    as32 = values.astype(np.float32)
+    expected = torch.from_numpy(as32).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(ov.round_narrow(as32.astype(np.float64), "bf16"), expected)
+
+
+def test_fp32_closed_form_tolerance_equals_published_value():
+    """The reference's check on its default inputs yields its published bound (bw1100 and H20)."""
+    golden = GOLDEN["vector_fp32"]
+    assert golden["max_abs_tolerance"] == GOLDEN["vector_fp32_h20"]["max_abs_tolerance"]
+    inputs, coefficients = ov.reference_inputs("fp32", 2048, np.random.default_rng(4))
+    output = ov.run_chains("fp32", inputs, coefficients, golden["iterations"])
+    result = ov.closed_form_check(inputs, output, coefficients, golden["iterations"], "fp32")
+    assert result["max_abs_tolerance"] == pytest.approx(golden["max_abs_tolerance"], rel=1e-12)
+    # The emulated error has the published magnitude (both are ~1e-4 and below the bound).
+    assert 0.2 * golden["max_abs_error"] < result["max_abs_error"] < golden["max_abs_tolerance"]
+    # A chain run with the wrong bias (b_6 instead of b_5) drifts well past the bound.
+    output[5] = ov.run_chains("fp32", inputs[5:6], coefficients[[0, 7]], golden["iterations"])[0]
+    with pytest.raises(AssertionError):
+        ov.closed_form_check(inputs, output, coefficients, golden["iterations"], "fp32")
+
+
+def test_fp64_closed_form_tolerance_equals_published_value():
+    golden = GOLDEN["vector_fp64"]
+    inputs, coefficients = ov.reference_inputs("fp64", 1024, np.random.default_rng(5))
+    output = ov.run_chains("fp64", inputs, coefficients, golden["iterations"])
+    result = ov.closed_form_check(inputs, output, coefficients, golden["iterations"], "fp64")
+    assert result["max_abs_tolerance"] == pytest.approx(golden["max_abs_tolerance"], rel=1e-12)
+    assert result["max_abs_error"] < golden["max_abs_tolerance"]
+    output[0, 0] += 1e-8  # the reference's own corruption check (tests/test_vector_dtypes.py:150-160)
+    with pytest.raises(AssertionError):
+        ov.closed_form_check(inputs, output, coefficients, golden["iterations"], "fp64")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_involution_is_exact_and_odd_iterations_reject_identity(dtype):
+    inputs, coefficients = ov.reference_inputs(dtype, 31, np.random.default_rng(6))
+    for iterations in (1, 2, 3, 32, 33):
+        output = ov.run_chains(dtype, inputs, coefficients, iterations)
+        result = ov.closed_form_check(inputs, output, coefficients, iterations, dtype)
+        assert result["max_abs_error"] == 0 and result["max_abs_tolerance"] == 0
+    with pytest.raises(AssertionError):
+        ov.closed_form_check(inputs, inputs, coefficients, 33, dtype)
+
+
+def test_int8_dot4_brute_force_matches_transition_table():
+    assert ov.signed_bytes(ov.pack_bytes(GOLDEN["int8_weights"]["weights"])) == GOLDEN["int8_weights"]["weights"]
+    inputs, coefficients = ov.reference_inputs("int8", 43, np.random.default_rng(7))
+    for iterations in (1, 2, 3, 32, 4096):
+        output = ov.run_chains("int8", inputs, coefficients, iterations)
+        ov.int8_transition_check(inputs, output, coefficients, iterations)
+    output[3, 7] += 1
+    with pytest.raises(AssertionError):
+        ov.int8_transition_check(inputs, output, coefficients, 4096)
+
+
+def test_int8_naive_recurrence_agrees_with_emulation():
+    inputs, coefficients = ov.reference_inputs("int8", 16, np.random.default_rng(8))
+    weights = ov.signed_bytes(coefficients[0])
+    state = inputs.astype(np.int64)
+    for _ in range(50):
+        state = ov.dot4_reference(state, weights) + coefficients[1:, None].astype(np.int64)
+    assert np.array_equal(ov.run_chains("int8", inputs, coefficients, 50), state)
+
+
+def test_operation_counts_match_published_rows():
+    for key in ("vector_fp32", "vector_fp32_h20"):
+        golden = GOLDEN[key]
+        assert ov.operation_count("fp32", golden["elements_per_chain"], golden["iterations"]) == golden["counted_flops"]
+    assert ov.operation_count("int8", 17, 32) == 8 * 8 * 17 * 32  # tests/test_vector_dtypes.py:46-57
+
+
+def test_baseline_inputs_bf16_are_the_degenerate_fixed_point():
+    """b = 0.999 rounds to 1.0 in bf16 and c = 1e-3 is below half an ulp, so states never move."""
+    inputs, coefficients = ov.baseline_inputs("bf16", 64, np.random.default_rng(9))
+    assert coefficients[0] == 1.0
+    assert np.array_equal(ov.run_chains("bf16", inputs, coefficients, 4096), inputs)
+
+
+# ---- tensor oracle ----------------------------------------------------------------------------
+
+def test_peak_tolerance_and_op_count_match_published_rows():
+    golden = GOLDEN["tensor_bf16_peak"]
+    assert ot.peak_tolerance("bf16", golden["config"]["block_k"], golden["iterations"]) == golden["atol"]
+    cfg = golden["config"]
+    assert ot.peak_operation_count(cfg["block_m"], cfg["block_n"], cfg["block_k"], golden["iterations"],
+                                   cfg["chains"], golden["blocks"]) == golden["operation_count"]
+    golden = GOLDEN["tensor_int8_peak"]
+    cfg = golden["config"]
+    assert ot.peak_tolerance("int8", cfg["block_k"], golden["iterations"]) == golden["atol"] == 0
+    assert ot.peak_operation_count(cfg["block_m"], cfg["block_n"], cfg["block_k"], golden["iterations"],
+                                   cfg["chains"], golden["blocks"]) == golden["operation_count"]
+    bounds = GOLDEN["peak_tolerance"]
+    tolerance = ot.peak_tolerance("bf16", bounds["bf16_block_k"], bounds["iterations"])
+    assert bounds["above"] < tolerance < bounds["below"]
+    assert ot.peak_tolerance("fp64", 16, 1024) < ot.peak_tolerance("fp32", 16, 1024)
+
+
+def test_e2m1_table_packing_and_scales():
+    golden = GOLDEN["e2m1_packing"]
+    codes = np.array(golden["codes"], dtype=np.uint8)
+    assert ot.pack_e2m1(codes).tolist() == golden["packed"]
+    assert np.array_equal(ot.unpack_e2m1(ot.pack_e2m1(codes)), codes)
+    for code, value in golden["values"].items():
+        assert ot.e2m1_decode(int(code)) == value
+    assert np.array_equal(ot.e2m1_decode(np.arange(16)), ot.E2M1_VALUES)
+    assert ot.e8m0_decode(127) == 1.0 and ot.e8m0_decode(128) == 2.0 and np.isnan(ot.e8m0_decode(255))
+
+
+def test_fp8_decoder_matches_torch_for_every_code():
+    import torch
+
+    codes = np.arange(256, dtype=np.uint8)
+    expected = torch.from_numpy(codes).view(torch.float8_e4m3fn).double().numpy()
+    got = ot.fp8_e4m3fn_decode(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(expected))
+    assert np.array_equal(got[~np.isnan(got)], expected[~np.isnan(expected)])
+    values = np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0, 1 / 16, 448.0])
+    assert np.array_equal(ot.fp8_e4m3fn_decode(ot.fp8_e4m3fn_encode_exact(values)), values)
+
+
+def test_peak_reference_is_iterations_times_the_tile_product():
+    rng = np.random.default_rng(10)
+    a = ot.ternary_lattice(rng, (2, 8, 16))
+    b = ot.ternary_lattice(rng, (2, 2, 16, 8))
+    reference = ot.peak_reference(a, b, 5)
+    brute = np.zeros_like(reference)
+    for c in range(2):
+        for w in range(2):
+            for i in range(8):
+                for j in range(8):
+                    brute[c, w, i, j] = 5 * sum(a[w, i, k] * b[c, w, k, j] for k in range(16))
+    assert np.array_equal(reference, brute)
+    wrong = reference.copy()
+    wrong[1, 1, 2, 3] += 1 / 256  # one lattice step, what a dropped dot changes
+    with pytest.raises(AssertionError):
+        ot.check_peak(wrong, reference, "bf16", 16, 5)
+
+
+# ---- memory oracle ----------------------------------------------------------------------------
+
+def test_bandwidth_traffic_matches_published_rows():
+    copy, read = GOLDEN["bandwidth"]["copy"], GOLDEN["bandwidth"]["read"]
+    assert memory.copy_traffic_bytes(copy["buffer_bytes"]) == copy["traffic_bytes"]
+    assert memory.read_traffic_bytes(read["buffer_bytes"], read["elements"], read["block_size"]) == read["traffic_bytes"]
+    assert memory.gbps(copy["traffic_bytes"], copy["median_ms"]) == pytest.approx(copy["gbps"])
+
+
+def test_block_sums_exact_on_integer_lattice_and_tolerance_rejects_errors():
+    rng = np.random.default_rng(11)
+    values = rng.integers(-8, 9, 4096 + 17).astype(np.float32)
+    sums = memory.block_sums(values, 1024)
+    assert sums.shape == (5,) and sums[-1] == values[4096:].sum()
+    assert memory.check_read(values, sums.astype(np.float32), 1024) == 0.0
+    bad = sums.copy()
+    bad[2] += 1.0
+    with pytest.raises(AssertionError):
+        memory.check_read(values, bad, 1024)
+    assert memory.cache_regime(2**30, 256 * 2**20, False) == ("larger_than_l2", True)
+    assert memory.cache_regime(512 * 2**20, 256 * 2**20, False) == ("cache_sensitive", False)
+    assert memory.cache_regime(2**30, 0, False) == ("unknown_l2", False)
+    assert math.isclose(memory.read_tolerance(np.ones(1024), 1024)[0], 1024 * 2 * 2**-23 * 10 + 1e-6)

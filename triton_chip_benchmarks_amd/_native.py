@@ -90,6 +90,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mb_tensor_peak_kernel_name": (ctypes.c_char_p, [_i32, ctypes.POINTER(PeakConfig)]),
     "mb_tensor_peak": (_i32, [_i32, ctypes.POINTER(PeakConfig), _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64,
                               _ptr, _u64, _u32, _u32, _ptr]),
+    "mb_vector_kernel_name": (ctypes.c_char_p, [_i32, _u32]),
+    "mb_vector_chains": (_i32, [_i32, _ptr, _ptr, _ptr, _u64, _u32, _u32, _u32, _u64, _u64, _u64, _ptr]),
 }
 
 _lock = threading.Lock()
