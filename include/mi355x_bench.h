@@ -152,6 +152,35 @@ int mb_tensor_peak(int format, const mb_peak_config* config, const void* a, uint
                    const void* scale_b, uint64_t scale_b_bytes, void* c, uint64_t c_bytes,
                    uint32_t blocks, uint32_t iterations, void* stream);
 
+/* ---- tensor: dense GEMM ---------------------------------------------------- */
+
+typedef struct mb_gemm_config {
+  uint32_t tile_m;  /* output rows per workgroup */
+  uint32_t tile_n;  /* output columns per workgroup */
+  uint32_t tile_k;  /* K elements staged through LDS per step */
+  uint32_t threads; /* workgroup size (output only) */
+} mb_gemm_config;
+
+/* Tile configurations compiled for `format` (see mb_tensor_peak_configs). */
+int mb_gemm_configs(int format, mb_gemm_config* out, int capacity);
+
+/* Registered kernel name of a GEMM configuration, or NULL. */
+const char* mb_gemm_kernel_name(int format, const mb_gemm_config* config);
+
+/* C = A . B with A row-major [m][k] and B column-major, i.e. stored [n][k]
+ * (both K-contiguous); C row-major [m][n] in the format's accumulator type
+ * (fp32; int32 for I8; fp64 for F64). MXFP4: A and B hold two E2M1 codes per
+ * byte along K (even k in the low nibble), scale_a [m][k/32] and scale_b
+ * [n][k/32] are E8M0. K * element bits must be a multiple of 128 (16-byte
+ * rows); other shapes are bounded by a checked kernel variant. group_m = 0
+ * selects the default band of 8 tile rows.
+ * Replaces: bench_tensor.py:172-209 (_gemm_kernel) and 235-246 (_launch),
+ * whose B is row-major [k][n]. */
+int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_bytes, const void* b,
+            uint64_t b_bytes, const void* scale_a, uint64_t scale_a_bytes, const void* scale_b,
+            uint64_t scale_b_bytes, void* c, uint64_t c_bytes, uint32_t m, uint32_t n, uint32_t k,
+            uint32_t group_m, void* stream);
+
 /* ---- vector: register-resident arithmetic chains ------------------------ */
 
 /* Vector chain kinds. Storage of input/output/coefficients per kind:

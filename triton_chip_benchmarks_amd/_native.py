@@ -70,6 +70,14 @@ class PeakConfig(ctypes.Structure):
         return {field: getattr(self, field) for field, _ in self._fields_}
 
 
+class GemmConfig(ctypes.Structure):
+    _fields_ = [("tile_m", ctypes.c_uint32), ("tile_n", ctypes.c_uint32), ("tile_k", ctypes.c_uint32),
+                ("threads", ctypes.c_uint32)]
+
+    def as_dict(self) -> dict:
+        return {field: getattr(self, field) for field, _ in self._fields_}
+
+
 # Matrix formats of the tensor entry points (MB_MATRIX_*).
 MATRIX_FORMATS = {"bf16": 0, "fp16": 1, "fp32": 2, "tf32": 3, "int8": 4, "fp64": 5, "fp8": 6, "fp4": 7}
 
@@ -90,6 +98,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mb_tensor_peak_kernel_name": (ctypes.c_char_p, [_i32, ctypes.POINTER(PeakConfig)]),
     "mb_tensor_peak": (_i32, [_i32, ctypes.POINTER(PeakConfig), _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64,
                               _ptr, _u64, _u32, _u32, _ptr]),
+    "mb_gemm_configs": (_i32, [_i32, ctypes.POINTER(GemmConfig), _i32]),
+    "mb_gemm_kernel_name": (ctypes.c_char_p, [_i32, ctypes.POINTER(GemmConfig)]),
+    "mb_gemm": (_i32, [_i32, ctypes.POINTER(GemmConfig), _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64,
+                       _u32, _u32, _u32, _u32, _ptr]),
     "mb_vector_kernel_name": (ctypes.c_char_p, [_i32, _u32]),
     "mb_vector_chains": (_i32, [_i32, _ptr, _ptr, _ptr, _u64, _u32, _u32, _u32, _u64, _u64, _u64, _ptr]),
 }
@@ -205,6 +217,39 @@ def tensor_peak(dtype: str, config: dict, a, b, c, blocks: int, iterations: int,
     call("mb_tensor_peak", MATRIX_FORMATS[dtype], ctypes.byref(peak_config(config)), a_ptr, a_bytes, b_ptr,
          b_bytes, sa_ptr, sa_bytes, sb_ptr, sb_bytes, c_ptr, c_bytes, blocks, iterations,
          stream_handle(stream))
+
+
+def gemm_configs(dtype: str) -> list[dict]:
+    """Compiled GEMM tiles of a matrix format."""
+    library = load()
+    code = MATRIX_FORMATS[dtype]
+    count = library.mb_gemm_configs(code, None, 0)
+    if count < 0:
+        check(count)
+    configs = (GemmConfig * max(count, 1))()
+    library.mb_gemm_configs(code, configs, count)
+    return [configs[index].as_dict() for index in range(count)]
+
+
+def _gemm_config(config: dict) -> GemmConfig:
+    return GemmConfig(config["tile_m"], config["tile_n"], config["tile_k"], int(config.get("threads", 0)))
+
+
+def gemm_kernel_name(dtype: str, config: dict) -> str | None:
+    name = load().mb_gemm_kernel_name(MATRIX_FORMATS[dtype], ctypes.byref(_gemm_config(config)))
+    return name.decode() if name else None
+
+
+def gemm(dtype: str, config: dict, a, b, c, m: int, n: int, k: int, scale_a=None, scale_b=None, group_m: int = 0,
+         stream=None) -> None:
+    """C = A . B^T-stored (both K-contiguous) on the current stream."""
+    a_ptr, a_bytes = _buffer(a)
+    b_ptr, b_bytes = _buffer(b)
+    sa_ptr, sa_bytes = _buffer(scale_a)
+    sb_ptr, sb_bytes = _buffer(scale_b)
+    c_ptr, c_bytes = _buffer(c)
+    call("mb_gemm", MATRIX_FORMATS[dtype], ctypes.byref(_gemm_config(config)), a_ptr, a_bytes, b_ptr, b_bytes,
+         sa_ptr, sa_bytes, sb_ptr, sb_bytes, c_ptr, c_bytes, m, n, k, group_m, stream_handle(stream))
 
 
 def stream_handle(stream=None) -> int | None:

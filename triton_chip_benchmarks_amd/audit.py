@@ -44,8 +44,8 @@ def registered_name(symbol: str) -> str | None:
         return f"tensor_peak_{_MFMA_FORMAT[op]}_{bm}x{bn}x{bk}_c{chains}_{'nk' if nk == '1' else 'kn'}"
     match = _GEMM_RE.search(symbol)
     if match:
-        op, bm, bn, bk, _wm, _wn, _flag = match.groups()
-        return f"gemm_{_MFMA_FORMAT[op]}_{bm}x{bn}x{bk}"
+        op, bm, bn, bk, _wm, _wn, checked = match.groups()
+        return f"gemm_{_MFMA_FORMAT[op]}_{bm}x{bn}x{bk}{'_checked' if checked == '1' else ''}"
     match = _COPY_RE.search(symbol)
     if match:
         unit, vpt, nt = match.groups()

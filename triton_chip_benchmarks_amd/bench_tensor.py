@@ -443,8 +443,8 @@ def build_parser():
                         help="resident MFMA repeats, 1..262144; FP8/FP4 maximum 4096 (default: 1024)")
     parser.add_argument("--blocks-per-sm", nargs="+", type=int, default=[1, 2, 4, 8],
                         help="launched workgroups per CU (default: 1 2 4 8)")
-    parser.add_argument("--sizes", nargs="+", type=int, default=[2048, 4096, 8192],
-                        help="square GEMM dimensions M=N=K (default: 2048 4096 8192)")
+    parser.add_argument("--sizes", nargs="+", type=int, default=None,
+                        help="square GEMM dimensions M=N=K (default: the BASELINE size of the format)")
     parser.add_argument("--dtype", choices=DTYPES, default="fp16",
                         help="matrix input format; TF32 uses FP32 storage; FP8 is E4M3FN and FP4 is OCP MX E2M1")
     parser.add_argument("--input-precision", choices=("ieee", "tf32"),
@@ -454,7 +454,7 @@ def build_parser():
     parser.add_argument("--tiles", nargs="+", help="restrict peak tiles, e.g. 128x128x64")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--quick", action="store_true",
-                        help="smoke test: one tile and 64 repeats, or GEMM dimensions 256/513")
+                        help="smoke test: one tile and 64 repeats, or GEMM dimensions 256/544")
     add_common_arguments(parser)
     return parser
 
@@ -482,6 +482,8 @@ def main(argv=None) -> None:
     parser = build_parser()
     args = parser.parse_args(argv)
     normalize_precision_args(parser, args)
+    args.sizes_given = args.sizes is not None
+    args.sizes = args.sizes or [2048, 4096, 8192]
     if any(size <= 0 for size in args.sizes):
         parser.error("--sizes values must be positive")
     if not 1 <= args.iterations <= 262144:
@@ -493,7 +495,7 @@ def main(argv=None) -> None:
     if args.dtype == "int8" and args.mode == "gemm" and any(size >= 2**24 for size in args.sizes):
         parser.error("INT8 GEMM requires K < 2**24 for an exact FP32 reference")
     if args.quick:
-        args.sizes = [256, 513]
+        args.sizes = [256, 544]
     metadata = setup_device(args)
     metadata.update(precision_descriptor(args.dtype, args.input_precision))
     reason = capability_reason(args)

@@ -1,0 +1,340 @@
+// Dense GEMM on the matrix cores (tensor rows' GEMM mode and BASELINE's
+// 8192^3 / 4096^3 / 16384^3 configurations).
+//
+// C[M][N] = A[M][K] . B[K][N] with A row-major and B column-major, so both
+// operands are K-contiguous in memory ("NT"); the accumulator type is the
+// instruction's (fp32, int32 for INT8, fp64 for FP64). MXFP4 operands carry
+// one E8M0 scale per 32 K elements: SA[M][K/32], SB[N][K/32].
+// Replaces the reference's _gemm_kernel (bench_tensor.py:172-209), whose B is
+// row-major; the MI355X kernel takes K-contiguous B (layout prepared outside
+// timing by the caller).
+//
+// Design:
+//   * a workgroup of WAVES_M x WAVES_N waves owns a BM x BN tile; each wave a
+//     (BM/WAVES_M) x (BN/WAVES_N) block of 32x32 (16x16 for FP64) MFMA tiles;
+//   * each K step stages BM x BK and BN x BK operand tiles from HBM into a
+//     padded, double-buffered LDS tile with 16-byte coalesced loads; the loads
+//     of step k+1 are in flight while the MFMAs of step k run, and one barrier
+//     per step separates the buffers;
+//   * workgroups are numbered XCD-first: the hardware deals consecutive
+//     workgroup ids round-robin over the 8 XCDs, so id i is remapped to the
+//     i/8-th tile of XCD i%8's contiguous share, and within that share tiles
+//     are walked in GROUP_M-row bands, keeping A and B panels hot in the XCD's L2;
+//   * CHECKED instantiations bound every load and store for ragged shapes.
+#include "mb_internal.h"
+#include "mb_mfma.h"
+
+namespace mb {
+namespace {
+
+constexpr int kXcds = 8;
+
+template <class Op, int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+struct GemmTile {
+  static constexpr int THREADS = 64 * WAVES_M * WAVES_N;
+  static constexpr int BK_BYTES = BK * Op::ELEM_BITS / 8;
+  static constexpr int STRIDE = BK_BYTES + 16;  // padded LDS row, keeps 16-byte alignment
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int TM = WM / Op::M, TN = WN / Op::N;
+  static constexpr int KSTEPS = BK_BYTES / MfmaGeometry<Op>::K_BYTES;
+  static constexpr int ROW_CHUNKS = BK_BYTES / 16;
+  static constexpr int A_CHUNKS = BM * ROW_CHUNKS / THREADS;  // 16-byte loads per thread per step
+  static constexpr int B_CHUNKS = BN * ROW_CHUNKS / THREADS;
+  static constexpr int BUFFER = (BM + BN) * STRIDE;
+  static constexpr int GROUPS = Op::SCALED ? BK / 32 : 0;
+  static_assert(BM * ROW_CHUNKS % THREADS == 0 && BN * ROW_CHUNKS % THREADS == 0, "whole loads per thread");
+  static_assert(BK_BYTES % MfmaGeometry<Op>::K_BYTES == 0, "BK must hold whole instructions");
+  static_assert(WM % Op::M == 0 && WN % Op::N == 0, "wave tile must hold whole instructions");
+};
+
+// Stage one K step of A and B into registers (global loads in flight).
+template <class T, bool CHECKED>
+__device__ __forceinline__ void load_step(i32x4 (&ra)[T::A_CHUNKS], i32x4 (&rb)[T::B_CHUNKS],
+                                          const uint8_t* a_tile, const uint8_t* b_tile, uint64_t row_bytes,
+                                          int rows_a, int rows_b, int64_t k_bytes_left) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < T::A_CHUNKS; ++i) {
+    const int c = i * T::THREADS + t;
+    const int row = c / T::ROW_CHUNKS, chunk = c % T::ROW_CHUNKS;
+    if (!CHECKED || (row < rows_a && chunk * 16 < k_bytes_left))
+      ra[i] = *reinterpret_cast<const i32x4*>(a_tile + row * row_bytes + chunk * 16);
+    else
+      ra[i] = i32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int i = 0; i < T::B_CHUNKS; ++i) {
+    const int c = i * T::THREADS + t;
+    const int row = c / T::ROW_CHUNKS, chunk = c % T::ROW_CHUNKS;
+    if (!CHECKED || (row < rows_b && chunk * 16 < k_bytes_left))
+      rb[i] = *reinterpret_cast<const i32x4*>(b_tile + row * row_bytes + chunk * 16);
+    else
+      rb[i] = i32x4{0, 0, 0, 0};
+  }
+}
+
+template <class T>
+__device__ __forceinline__ void store_step(uint8_t* buffer, const i32x4 (&ra)[T::A_CHUNKS],
+                                           const i32x4 (&rb)[T::B_CHUNKS], int bm) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < T::A_CHUNKS; ++i) {
+    const int c = i * T::THREADS + t;
+    *reinterpret_cast<i32x4*>(buffer + (c / T::ROW_CHUNKS) * T::STRIDE + (c % T::ROW_CHUNKS) * 16) = ra[i];
+  }
+  uint8_t* b_buffer = buffer + bm * T::STRIDE;
+#pragma unroll
+  for (int i = 0; i < T::B_CHUNKS; ++i) {
+    const int c = i * T::THREADS + t;
+    *reinterpret_cast<i32x4*>(b_buffer + (c / T::ROW_CHUNKS) * T::STRIDE + (c % T::ROW_CHUNKS) * 16) = rb[i];
+  }
+}
+
+template <class Op, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool CHECKED>
+__global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
+    gemm_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__ SA,
+                const uint8_t* __restrict__ SB, typename Op::Out* __restrict__ C, int M, int N, int K,
+                int group_m) {
+  using T = GemmTile<Op, BM, BN, BK, WAVES_M, WAVES_N>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * T::BUFFER];
+
+  // XCD-first workgroup numbering, then GROUP_M bands of tiles.
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int count = gridDim.x;
+  int pid = blockIdx.x;
+  if (count % kXcds == 0) pid = (pid % kXcds) * (count / kXcds) + pid / kXcds;
+  const int band = group_m * tiles_n;
+  const int first_m = (pid / band) * group_m;
+  const int rows_in_band = min(tiles_m - first_m, group_m);
+  const int tile_m = first_m + (pid % band) % rows_in_band;
+  const int tile_n = (pid % band) / rows_in_band;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const uint64_t row_bytes = static_cast<uint64_t>(K) * Op::ELEM_BITS / 8;
+  const uint8_t* a_tile = A + m0 * row_bytes;
+  const uint8_t* b_tile = B + n0 * row_bytes;
+  const int rows_a = M - m0, rows_b = N - n0;
+  const int k_steps = (K + BK - 1) / BK;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int lrow = lane % Op::M, lgroup = lane / Op::M;
+  constexpr int KB = MfmaGeometry<Op>::K_BYTES;
+  const int scale_cols = Op::SCALED ? K / 32 : 0;
+
+  typename Op::Acc acc[T::TM][T::TN];
+#pragma unroll
+  for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn) acc[tm][tn] = typename Op::Acc{};
+
+  i32x4 ra[T::A_CHUNKS], rb[T::B_CHUNKS];
+  load_step<T, CHECKED>(ra, rb, a_tile, b_tile, row_bytes, rows_a, rows_b, static_cast<int64_t>(row_bytes));
+  store_step<T>(lds, ra, rb, BM);
+  __syncthreads();
+
+  for (int kt = 0; kt < k_steps; ++kt) {
+    uint8_t* current = lds + (kt & 1) * T::BUFFER;
+    const bool more = kt + 1 < k_steps;
+    if (more)
+      load_step<T, CHECKED>(ra, rb, a_tile + (kt + 1) * T::BK_BYTES, b_tile + (kt + 1) * T::BK_BYTES, row_bytes,
+                            rows_a, rows_b, static_cast<int64_t>(row_bytes) - (kt + 1) * T::BK_BYTES);
+    // E8M0 scales of this step: column kt*BK/32 + ks*LANE_GROUPS + group.
+    int sa[T::TM][T::KSTEPS], sb[T::TN][T::KSTEPS];
+    if constexpr (Op::SCALED) {
+#pragma unroll
+      for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+        for (int ks = 0; ks < T::KSTEPS; ++ks) {
+          const int row = m0 + wm * T::WM + tm * Op::M + lrow;
+          const int col = kt * T::GROUPS + ks * MfmaGeometry<Op>::LANE_GROUPS + lgroup;
+          sa[tm][ks] = (!CHECKED || (row < M && col < scale_cols)) ? SA[static_cast<int64_t>(row) * scale_cols + col]
+                                                                    : 127;
+        }
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+        for (int ks = 0; ks < T::KSTEPS; ++ks) {
+          const int col_n = n0 + wn * T::WN + tn * Op::N + lrow;
+          const int col = kt * T::GROUPS + ks * MfmaGeometry<Op>::LANE_GROUPS + lgroup;
+          sb[tn][ks] = (!CHECKED || (col_n < N && col < scale_cols))
+                           ? SB[static_cast<int64_t>(col_n) * scale_cols + col]
+                           : 127;
+        }
+    } else {
+#pragma unroll
+      for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+        for (int ks = 0; ks < T::KSTEPS; ++ks) sa[tm][ks] = 0;
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+        for (int ks = 0; ks < T::KSTEPS; ++ks) sb[tn][ks] = 0;
+    }
+    const uint8_t* a_lds = current + (wm * T::WM + lrow) * T::STRIDE + lgroup * Op::LANE_BYTES;
+    const uint8_t* b_lds = current + (BM + wn * T::WN + lrow) * T::STRIDE + lgroup * Op::LANE_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < T::KSTEPS; ++ks) {
+      typename Op::Frag a[T::TM], b[T::TN];
+#pragma unroll
+      for (int tm = 0; tm < T::TM; ++tm) a[tm] = load_frag<typename Op::Frag>(a_lds + tm * Op::M * T::STRIDE + ks * KB);
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn) b[tn] = load_frag<typename Op::Frag>(b_lds + tn * Op::N * T::STRIDE + ks * KB);
+#pragma unroll
+      for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < T::TN; ++tn)
+          acc[tm][tn] = Op::mma(a[tm], b[tn], acc[tm][tn], sa[tm][ks], sb[tn][ks]);
+    }
+    if (more) store_step<T>(lds + ((kt + 1) & 1) * T::BUFFER, ra, rb, BM);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+      for (int r = 0; r < Op::ACC_REGS; ++r) {
+        const int row = m0 + wm * T::WM + tm * Op::M + Op::out_row(lane, r);
+        const int col = n0 + wn * T::WN + tn * Op::N + (lane % Op::N);
+        if (!CHECKED || (row < M && col < N)) C[static_cast<int64_t>(row) * N + col] = acc[tm][tn][r];
+      }
+}
+
+using GemmLauncher = void (*)(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, void*, int, int, int,
+                              int, uint32_t, hipStream_t);
+
+template <class Op, int BM, int BN, int BK, int WM, int WN, bool CHECKED>
+void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m, int n,
+                 int k, int group_m, uint32_t blocks, hipStream_t stream) {
+  gemm_kernel<Op, BM, BN, BK, WM, WN, CHECKED><<<dim3(blocks), dim3(64 * WM * WN), 0, stream>>>(
+      a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+}
+
+struct GemmVariant {
+  int format;
+  mb_gemm_config config;
+  const char* name;
+  const void* kernel;
+  GemmLauncher launch;
+  GemmLauncher launch_checked;
+  int out_bytes;
+  int elem_bits;
+};
+
+#define MB_GEMM(FMT, OP, BM, BN, BK, WM, WN, NAME)                                                           \
+  GemmVariant{FMT,                                                                                           \
+              mb_gemm_config{BM, BN, BK, 64 * WM * WN},                                                      \
+              NAME,                                                                                          \
+              reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, false>),                     \
+              launch_gemm<OP, BM, BN, BK, WM, WN, false>,                                                    \
+              launch_gemm<OP, BM, BN, BK, WM, WN, true>,                                                     \
+              static_cast<int>(sizeof(typename OP::Out)),                                                    \
+              OP::ELEM_BITS}
+
+const GemmVariant kGemmVariants[] = {
+    MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 256, 64, 2, 2, "gemm_bf16_256x256x64"),
+    MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
+    MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
+    MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 256, 64, 2, 2, "gemm_f16_256x256x64"),
+    MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
+    MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
+    MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 256, 128, 2, 2, "gemm_fp8_256x256x128"),
+    MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
+    MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
+    MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 256, 128, 2, 2, "gemm_i8_256x256x128"),
+    MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
+    MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
+    MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
+    MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, "gemm_mxfp4_128x128x256"),
+    MB_GEMM(MB_MATRIX_F64, MfmaF64, 128, 128, 16, 2, 2, "gemm_f64_128x128x16"),
+    MB_GEMM(MB_MATRIX_F64, MfmaF64, 64, 64, 16, 2, 2, "gemm_f64_64x64x16"),
+    MB_GEMM(MB_MATRIX_F32, MfmaF32, 128, 128, 32, 2, 2, "gemm_f32_128x128x32"),
+};
+
+struct GemmRegistrar {
+  GemmRegistrar() {
+    for (const auto& variant : kGemmVariants) register_kernel(variant.name, variant.kernel);
+  }
+};
+const GemmRegistrar kGemmRegistrar;
+
+const GemmVariant* find_gemm(int format, const mb_gemm_config* config) {
+  for (const auto& variant : kGemmVariants) {
+    const mb_gemm_config& v = variant.config;
+    if (variant.format == format && v.tile_m == config->tile_m && v.tile_n == config->tile_n &&
+        v.tile_k == config->tile_k)
+      return &variant;
+  }
+  return nullptr;
+}
+
+}  // namespace
+}  // namespace mb
+
+extern "C" {
+
+int mb_gemm_configs(int format, mb_gemm_config* out, int capacity) {
+  using namespace mb;
+  if (int rc = matrix_format_check(format, "mb_gemm_configs")) return rc;
+  int count = 0;
+  for (const auto& variant : kGemmVariants) {
+    if (variant.format != format) continue;
+    if (out != nullptr && count < capacity) out[count] = variant.config;
+    ++count;
+  }
+  return count;
+}
+
+const char* mb_gemm_kernel_name(int format, const mb_gemm_config* config) {
+  if (config == nullptr) return nullptr;
+  const mb::GemmVariant* variant = mb::find_gemm(format, config);
+  return variant ? variant->name : nullptr;
+}
+
+int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_bytes, const void* b,
+            uint64_t b_bytes, const void* scale_a, uint64_t scale_a_bytes, const void* scale_b,
+            uint64_t scale_b_bytes, void* c, uint64_t c_bytes, uint32_t m, uint32_t n, uint32_t k,
+            uint32_t group_m, void* stream) {
+  using namespace mb;
+  if (int rc = matrix_format_check(format, "mb_gemm")) return rc;
+  if (config == nullptr) return fail(MB_ERR_INVALID, "mb_gemm: config is NULL");
+  const GemmVariant* variant = find_gemm(format, config);
+  if (variant == nullptr)
+    return fail(MB_ERR_INVALID, "mb_gemm: no kernel for format %d with tile %ux%ux%u (see mb_gemm_configs)", format,
+                config->tile_m, config->tile_n, config->tile_k);
+  if (m == 0 || n == 0 || k == 0) return fail(MB_ERR_INVALID, "mb_gemm: empty problem %ux%ux%u", m, n, k);
+  if (m > 0x7fffffffu || n > 0x7fffffffu || k > 0x7fffffffu)
+    return fail(MB_ERR_INVALID, "mb_gemm: dimensions exceed 2^31-1");
+  if (format == MB_MATRIX_MXFP4 && k % 32)
+    return fail(MB_ERR_INVALID, "mb_gemm: MXFP4 needs K to be a multiple of the 32-element scale group");
+  const uint64_t row_bits = static_cast<uint64_t>(k) * variant->elem_bits;
+  if (row_bits % 128)
+    return fail(MB_ERR_INVALID, "mb_gemm: K*element size must be a multiple of 16 bytes (rows are 16-byte loads)");
+  const uint64_t row_bytes = row_bits / 8;
+  if (a == nullptr || b == nullptr || c == nullptr) return fail(MB_ERR_INVALID, "mb_gemm: NULL operand");
+  if (a_bytes < m * row_bytes || b_bytes < n * row_bytes ||
+      c_bytes < static_cast<uint64_t>(m) * n * variant->out_bytes)
+    return fail(MB_ERR_INVALID, "mb_gemm: buffers too small for %ux%ux%u", m, n, k);
+  if (!aligned(a, 16) || !aligned(b, 16) || !aligned(c, 16))
+    return fail(MB_ERR_ALIGNMENT, "mb_gemm: A, B and C must be 16-byte aligned");
+  if (format == MB_MATRIX_MXFP4) {
+    if (scale_a == nullptr || scale_b == nullptr)
+      return fail(MB_ERR_INVALID, "mb_gemm: MXFP4 needs E8M0 scales for A and B");
+    if (scale_a_bytes < static_cast<uint64_t>(m) * (k / 32) || scale_b_bytes < static_cast<uint64_t>(n) * (k / 32))
+      return fail(MB_ERR_INVALID, "mb_gemm: scale buffers too small ([M|N][K/32] bytes needed)");
+  }
+  const mb_gemm_config& v = variant->config;
+  const uint64_t tiles = static_cast<uint64_t>((m + v.tile_m - 1) / v.tile_m) * ((n + v.tile_n - 1) / v.tile_n);
+  if (tiles > 0x7fffffffull) return fail(MB_ERR_INVALID, "mb_gemm: too many tiles");
+  const bool exact = m % v.tile_m == 0 && n % v.tile_n == 0 && k % v.tile_k == 0;
+  const int group = group_m ? static_cast<int>(group_m) : 8;
+  GemmLauncher launch = exact ? variant->launch : variant->launch_checked;
+  launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
+         static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), group,
+         static_cast<uint32_t>(tiles), static_cast<hipStream_t>(stream));
+  return launch_status(variant->name);
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+"""Dense GEMM mode of the tensor benchmark (bench_tensor.py --mode gemm).
+
+Follows the reference's run_gemm (bench_tensor.py:1509-1595): per size and
+tile, validate C against a full-precision reference, then time the kernel and
+report 2*M*N*K operations. Operands follow BASELINE.json's GEMM configurations:
+  bf16/fp16/fp32/fp64  N(0, 1) from the seed; normwise relative tolerance
+                       (1e-2 for bf16/fp16, 1e-5 for fp32, 1e-12 for fp64)
+  fp8 (E4M3FN)         values from {+-0.5, +-1, +-2}; every product and partial
+                       sum is exact in fp32, so C must match bit for bit
+  int8                 uniform integers in [-8, 8]; exact int32
+  fp4 (MXFP4)          E2M1 codes uniform over all 16 values, E8M0 scale 127
+                       for every 32-element group; exact in fp32
+B is stored column-major ([N][K]), both operands K-contiguous. The reference
+is a float64 torch.matmul on the device, exact on the integer-valued sets.
+"""
+
+from __future__ import annotations
+
+from . import _native, audit, formats, roofline
+from .common import available_memory_bytes, emit_results, emit_unsupported, measure
+
+DEFAULT_SIZES = {"bf16": [8192], "fp16": [8192], "fp32": [8192], "fp8": [8192], "int8": [8192], "fp64": [4096],
+                 "fp4": [16384]}
+TOLERANCE = {"bf16": 1e-2, "fp16": 1e-2, "fp32": 1e-5, "fp64": 1e-12, "fp8": 0.0, "int8": 0.0, "fp4": 0.0}
+INPUT_PATTERN = {
+    "bf16": "N(0,1) values rounded to bf16", "fp16": "N(0,1) values rounded to fp16", "fp32": "N(0,1)",
+    "fp64": "N(0,1)", "fp8": "uniform over {+-0.5, +-1, +-2} (E4M3FN exact)", "int8": "uniform integers in [-8, 8]",
+    "fp4": "E2M1 codes uniform over all 16 values, E8M0 scale 127 (2^0) per 32 K elements"}
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def gemm_inputs(dtype: str, m: int, n: int, k: int, device, seed: int = 0):
+    """(a, b, c, scales, a_values, b_values): b stored [n][k]; *_values are float64 [.., k] views."""
+    torch = _torch()
+    generator = torch.Generator(device=device).manual_seed(seed)
+    scales = None
+    if dtype == "fp4":
+        codes_a = torch.randint(0, 16, (m, k), device=device, generator=generator, dtype=torch.uint8)
+        codes_b = torch.randint(0, 16, (n, k), device=device, generator=generator, dtype=torch.uint8)
+        a, b = formats.pack_e2m1_pairs(codes_a), formats.pack_e2m1_pairs(codes_b)
+        scales = (torch.full((m, k // 32), formats.E8M0_UNIT_SCALE, dtype=torch.uint8, device=device),
+                  torch.full((n, k // 32), formats.E8M0_UNIT_SCALE, dtype=torch.uint8, device=device))
+        a_values, b_values = formats.e2m1_decode(codes_a), formats.e2m1_decode(codes_b)
+        del codes_a, codes_b
+    elif dtype == "fp8":
+        palette = torch.tensor([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], device=device)
+        a = palette[torch.randint(0, 6, (m, k), device=device, generator=generator)].to(torch.float8_e4m3fn)
+        b = palette[torch.randint(0, 6, (n, k), device=device, generator=generator)].to(torch.float8_e4m3fn)
+        a_values, b_values = a.double(), b.double()
+    elif dtype == "int8":
+        a = torch.randint(-8, 9, (m, k), device=device, generator=generator, dtype=torch.int8)
+        b = torch.randint(-8, 9, (n, k), device=device, generator=generator, dtype=torch.int8)
+        a_values, b_values = a.double(), b.double()
+    else:
+        store = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32, "fp64": torch.float64}[dtype]
+        a = torch.randn((m, k), device=device, generator=generator, dtype=torch.float64).to(store)
+        b = torch.randn((n, k), device=device, generator=generator, dtype=torch.float64).to(store)
+        a_values, b_values = a.double(), b.double()
+    out = torch.int32 if dtype == "int8" else torch.float64 if dtype == "fp64" else torch.float32
+    c = torch.empty((m, n), dtype=out, device=device)
+    return a, b, c, scales, a_values, b_values
+
+
+def reference(a_values, b_values):
+    """C = A . B in float64 (B given [n][k])."""
+    return _torch().matmul(a_values, b_values.t().contiguous())
+
+
+def validate(c, ref, dtype: str) -> dict:
+    """Exact for fp8/int8/fp4; normwise max|C-R| / max|R| for the others."""
+    torch = _torch()
+    error = (c.double() - ref).abs().max().item()
+    scale = ref.abs().max().item() or 1.0
+    tolerance = TOLERANCE[dtype]
+    passed = error <= tolerance * scale if tolerance else error == 0.0
+    if not passed or not torch.isfinite(c.double()).all().item():
+        raise RuntimeError(f"GEMM correctness failed ({dtype}): max_abs_error={error:.6g}, "
+                           f"normwise={error / scale:.3g}, tolerance={tolerance:g}")
+    return {"passed": True, "max_abs_error": error, "normwise_relative_error": error / scale,
+            "tolerance": tolerance, "tolerance_kind": "exact" if not tolerance else "normwise relative",
+            "reference": "FP64 torch.matmul on the device (exact for the integer-valued operand sets)"}
+
+
+def run_gemm(args, metadata: dict, device) -> None:
+    from .bench_tensor import accumulator_name, precision_descriptor, rates
+
+    torch = _torch()
+    dtype = args.dtype
+    if args.input_precision == "tf32":
+        emit_unsupported("tensor", metadata, args, "gfx950 has no TF32 matrix instruction")
+        return
+    sizes = args.sizes if getattr(args, "sizes_given", False) else DEFAULT_SIZES[dtype]
+    if args.quick:
+        sizes = [256, 512]
+    candidates = _native.gemm_configs(dtype)
+    if args.tiles:
+        wanted = {tuple(int(x) for x in tile.split("x")) for tile in args.tiles}
+        candidates = [c for c in candidates if (c["tile_m"], c["tile_n"], c["tile_k"]) in wanted]
+    if args.quick:
+        candidates = candidates[:1]
+    unit = "TOPS" if dtype == "int8" else "TFLOP/s"
+    peak_value = roofline.PEAKS[f"tensor_{dtype}"][0]
+    print(f"\nMatrix GEMM: {dtype} inputs ({INPUT_PATTERN[dtype]}), {accumulator_name(dtype).upper()} "
+          "accumulate/output, B column-major; 2*M*N*K operations")
+    print(f"  N        tile M/N/K   median ms  median {unit}  peak {unit}  % peak   error")
+    rows = []
+    for size in sizes:
+        free = available_memory_bytes()
+        required = size * size * 48
+        if free is not None and required > 0.8 * free:
+            raise RuntimeError(f"N={size} needs about {required / 2**30:.1f} GiB; reduce --sizes")
+        a, b, c, scales, a_values, b_values = gemm_inputs(dtype, size, size, size, device, args.seed)
+        ref = reference(a_values, b_values)
+        del a_values, b_values
+        for config in candidates:
+            kernel = _native.gemm_kernel_name(dtype, config)
+            c.fill_(-2**31 if dtype == "int8" else float("nan"))
+
+            def run(config=config):
+                _native.gemm(dtype, config, a, b, c, size, size, size, *(scales or (None, None)))
+
+            run()
+            torch.cuda.synchronize()
+            correctness = validate(c, ref, dtype)
+            info = dict(audit.resources(kernel))
+            info.update(audit.audit_tensor(audit.instructions(kernel), dtype, args.input_precision))
+            if info.get("register_spills"):
+                rows.append({"mode": "gemm", "m": size, "n": size, "k": size, "dtype": dtype, "config": config,
+                             "status": "skipped", "reason": "configuration spills registers"})
+                continue
+            timing = measure(run, args)
+            row_rates = rates(2 * size**3, timing, dtype)
+            descriptor = precision_descriptor(dtype, args.input_precision)
+            row = {"mode": "gemm", "m": size, "n": size, "k": size, "dtype": dtype,
+                   "measurement_kind": f"{descriptor['math_mode']}_gemm" if dtype in ("fp32", "fp64")
+                   else "dense_tensor_gemm",
+                   "execution_kind": info["execution_kind"],
+                   "precision_verified": info["instruction_precision_verified"],
+                   "accumulator_dtype": accumulator_name(dtype), "output_dtype": accumulator_name(dtype),
+                   "layout": "A row-major, B column-major (both K-contiguous)", "input_pattern": INPUT_PATTERN[dtype],
+                   **descriptor, **row_rates,
+                   "config": {"block_m": config["tile_m"], "block_n": config["tile_n"], "block_k": config["tile_k"],
+                              "threads": config["threads"]},
+                   "kernel": kernel, "status": "ok", "correctness": correctness, "compiled": info,
+                   "roofline": roofline.describe(f"tensor_{dtype}", row_rates["peak_teraops_per_second"]),
+                   **timing}
+            rows.append(row)
+            print(f"{size:5d}   {config['tile_m']:>4}/{config['tile_n']}/{config['tile_k']:<4} "
+                  f"{timing['median_ms']:10.4f} {row_rates['median_teraops_per_second']:12.2f} "
+                  f"{row_rates['peak_teraops_per_second']:10.2f} "
+                  f"{100 * row_rates['peak_teraops_per_second'] / peak_value:7.1f}   "
+                  f"{correctness['max_abs_error']:.3g}", flush=True)
+        del a, b, c, ref
+    from .bench_tensor import emit_tensor_results
+
+    emit_tensor_results(metadata, args, rows)
