@@ -45,7 +45,7 @@ _DETAIL_KEYS = ("execution_kind", "native_tensor_verified", "native_arithmetic_v
                 "assembly_audit", "assembly_audit_note", "arithmetic_dtype", "includes_unpacking",
                 "input_storage_dtype", "accumulator_dtype", "output_dtype", "operation",
                 "measurement_kind", "timing_method", "timing_fallback_reason",
-                "instruction", "kernel")
+                "kernel", "tensor_instruction_types", "amdgcn_instruction_types")
 _CONFIGURATION_KEYS = ("config", "block_size", "num_warps", "unroll", "blocks_per_sm", "blocks",
                        "iterations", "pattern", "buffer_mib", "cache_regime", "peak_eligible",
                        "block_threads", "vectors_per_thread", "grid_blocks", "nontemporal", "variant")
