@@ -1,0 +1,163 @@
+"""CPU tests of the gfx950 instruction audit, on synthetic listings and on the built library.
+
+The reference refuses to call a rate native unless the compiled kernel issues
+the format's own instruction (bench_tensor.py:984-1146,
+bench_vector.py:623-799). Here the audited text is the disassembly of the
+code objects inside libmi355x_bench.so, so these tests check the kernels the
+GPU actually runs: each resident-peak kernel's timed loop issues only its
+format's MFMA plus scalar loop control, each vector kernel issues its native
+VALU instruction, nothing spills, and no packed-FP32 VALU form is emitted.
+"""
+
+from __future__ import annotations
+
+import re
+
+import pytest
+
+from triton_chip_benchmarks_amd import _native, audit
+from triton_chip_benchmarks_amd import build as native_build
+
+FORMAT_OF = {"bf16": "bf16", "f16": "fp16", "i8": "int8", "fp8": "fp8", "mxfp4": "fp4", "f32": "fp32",
+             "f64": "fp64"}
+PEAK_INSTRUCTION = {"bf16": "v_mfma_f32_32x32x16_bf16", "fp16": "v_mfma_f32_32x32x16_f16",
+                    "int8": "v_mfma_i32_32x32x32_i8", "fp8": "v_mfma_f32_32x32x64_f8f6f4",
+                    "fp4": "v_mfma_scale_f32_32x32x64_f8f6f4", "fp32": "v_mfma_f32_32x32x2_f32",
+                    "fp64": "v_mfma_f64_16x16x4_f64"}
+VECTOR_INSTRUCTION = {"f32": ("fp32", "v_fma_f32"), "f64": ("fp64", "v_fma_f64"), "f16": ("fp16", "v_pk_fma_f16"),
+                      "bf16dot": ("bf16", "v_dot2_f32_bf16"), "dot4": ("int8", "v_dot4_i32_i8")}
+
+
+@pytest.fixture(scope="module")
+def listing():
+    if not native_build.DISASSEMBLY.exists():
+        pytest.fail(f"{native_build.DISASSEMBLY} is missing: run __graft_entry__.build() first")
+    return audit.symbols()
+
+
+def _peak_format(name):
+    return FORMAT_OF[name.split("_")[2]]
+
+
+# ---- synthetic listings -----------------------------------------------------------
+
+def test_tensor_rules_accept_each_native_format_and_reject_the_others():
+    lines = {fmt: [f"{inst} a[0:15], v[0:1], v[2:3], a[0:15]"] for fmt, inst in PEAK_INSTRUCTION.items()}
+    lines["fp4"] = ["v_mfma_scale_f32_32x32x64_f8f6f4 a[0:15], v[0:7], v[8:15], a[0:15], v16, v17 "
+                    "op_sel_hi:[0,0,0] cbsz:4 blgp:4"]
+    for fmt in PEAK_INSTRUCTION:
+        result = audit.audit_tensor(lines[fmt], fmt)
+        assert result["native_tensor_verified"] and result["execution_kind"] == "tensor"
+        for other in PEAK_INSTRUCTION:
+            if other != fmt:
+                with pytest.raises(audit.TensorAuditError):
+                    audit.audit_tensor(lines[fmt], other)
+
+
+def test_fp8_rule_rejects_a_non_default_operand_format():
+    for modifier in ("cbsz:1", "blgp:2", "cbsz:4 blgp:4"):
+        with pytest.raises(audit.TensorAuditError):
+            audit.audit_tensor([f"v_mfma_f32_32x32x64_f8f6f4 a[0:15], v[0:7], v[8:15], a[0:15] {modifier}"], "fp8")
+
+
+def test_fp4_rule_needs_both_operands_in_e2m1():
+    for modifier in ("cbsz:4", "blgp:4", ""):
+        with pytest.raises(audit.TensorAuditError):
+            audit.audit_tensor([f"v_mfma_scale_f32_32x32x64_f8f6f4 a[0:15], v[0:7], v[8:15], a[0:15], v1, v2 "
+                                f"{modifier}"], "fp4")
+
+
+def test_tf32_is_never_verified_without_xf32_instructions():
+    with pytest.raises(audit.TensorAuditError):
+        audit.audit_tensor(["v_mfma_f32_32x32x2_f32 a[0:15], v0, v1, a[0:15]"], "fp32", "tf32")
+    with pytest.raises(audit.TensorAuditError):
+        audit.audit_tensor(["v_mfma_f32_32x32x4_xf32 a[0:15], v[0:1], v[2:3], a[0:15]"], "fp32", "ieee")
+
+
+def test_fp64_without_mfma_is_simt_and_no_instruction_is_an_error():
+    result = audit.audit_tensor(["v_fma_f64 v[0:1], v[2:3], v[4:5], v[0:1]"], "fp64")
+    assert (result["execution_kind"], result["native_tensor_verified"]) == ("simt", False)
+    with pytest.raises(audit.TensorAuditError):
+        audit.audit_tensor(["v_add_f32 v0, v1, v2"], "bf16")
+
+
+def test_vector_rules():
+    assert audit.audit_vector(["v_dot4_i32_i8 v0, v0, v1, v2"], "int8", "dp4a")["native_arithmetic_verified"]
+    assert audit.audit_vector(["v_dot2_f32_bf16 v0, v1, v2, v3"], "bf16", "dot2")["native_arithmetic_verified"]
+    promoted = audit.audit_vector(["v_fma_f32 v0, v1, v2, v3", "v_cvt_pk_bf16_f32 v0, v0, v4"], "bf16", "fma")
+    assert promoted["native_arithmetic_verified"] is False and promoted["amdgcn_arithmetic_promoted"]
+    with pytest.raises(audit.VectorAuditError):
+        audit.audit_vector(["v_mul_lo_u32 v0, v1, v2", "v_add_u32 v0, v0, v3"], "int8", "dp4a")
+    with pytest.raises(audit.VectorAuditError):
+        audit.audit_vector(["v_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]",
+                            "v_fma_f32 v0, v1, v2, v3"], "fp32", "fma")
+
+
+def test_registered_names_follow_the_mangled_template_arguments():
+    symbol = "_ZN2mb12_GLOBAL__N_118tensor_peak_kernelINS_8MfmaBf16ELi128ELi128ELi64ELi2ELi2ELi2ELb0EEEvPKh"
+    assert audit.registered_name(symbol) == "tensor_peak_bf16_128x128x64_c2_kn"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_111gemm_kernelINS_9MfmaMxfp4ELi128ELi128ELi256ELi2ELi2ELb1EEEv") \
+        == "gemm_mxfp4_128x128x256_checked"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIDv4_jLi1ELb1EEEv") == "copy_dwordx4_vpt1_nt"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
+    assert audit.registered_name("unrelated_symbol") is None
+
+
+# ---- the built library -----------------------------------------------------------
+
+def test_every_registered_kernel_is_in_the_audited_code_object(listing):
+    registered = set(_native.kernel_names())
+    assert registered, "the library registry is empty"
+    assert registered <= set(listing), sorted(registered - set(listing))
+
+
+def test_every_peak_kernel_runs_only_its_mfma_in_the_timed_loop(listing):
+    peak = [name for name in listing if name.startswith("tensor_peak_")]
+    assert len(peak) >= 40
+    for name in peak:
+        fmt = _peak_format(name)
+        result = audit.audit_tensor(audit.instructions(name), fmt)
+        assert result["tensor_instruction_types"] == [PEAK_INSTRUCTION[fmt]], name
+        summary = audit.loop_summary(name)
+        assert summary["timed_loop_matrix_types"] == [PEAK_INSTRUCTION[fmt]], name
+        assert summary["timed_loop_matrix_instructions"] >= 2, name
+        # Only scalar loop control and waits beside the MFMAs; FP64 also moves
+        # accumulator halves between AGPRs and VGPRs.
+        allowed = {"v_accvgpr_read_b32", "v_accvgpr_write_b32"} if fmt == "fp64" else set()
+        assert set(summary["timed_loop_vector_memory_or_alu"]) <= allowed, (name, summary)
+
+
+def test_every_gemm_kernel_uses_its_format_mfma(listing):
+    gemm = [name for name in listing if name.startswith("gemm_")]
+    assert gemm
+    for name in gemm:
+        fmt = FORMAT_OF[name.split("_")[1]]
+        result = audit.audit_tensor(audit.instructions(name), fmt)
+        assert result["tensor_instruction_types"] == [PEAK_INSTRUCTION[fmt]], name
+
+
+def test_every_vector_kernel_issues_its_native_instruction_and_no_mfma(listing):
+    vector = [name for name in listing if name.startswith("vector_")]
+    assert vector
+    for name in vector:
+        kind = re.match(r"vector_(\w+?)_u\d+$", name).group(1)
+        lines = audit.instructions(name)
+        if kind == "bf16fma":
+            result = audit.audit_vector(lines, "bf16", "fma")
+            assert result["native_arithmetic_verified"] is False
+            continue
+        dtype, instruction = VECTOR_INSTRUCTION[kind]
+        result = audit.audit_vector(lines, dtype, "native")
+        assert instruction in result["amdgcn_instruction_types"], (name, result)
+
+
+def test_no_kernel_spills_or_uses_scratch(listing):
+    for name in listing:
+        info = audit.resources(name)
+        assert info["register_spills"] == 0, (name, info)
+        assert not info["scratch_bytes"], (name, info)
+
+
+def test_no_packed_fp32_valu_anywhere():
+    text = native_build.DISASSEMBLY.read_text()
+    assert not re.search(r"\bv_pk_(?:add|mul|fma|mov)_f32\b", text)

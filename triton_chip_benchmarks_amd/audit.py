@@ -125,6 +125,66 @@ def instructions(name: str, disassembly: Path | None = None) -> list[str]:
     return _disassembly(str(path))[mapping[name]]
 
 
+_ADDRESS_RE = re.compile(r"//\s*([0-9A-Fa-f]+):")
+_TARGET_RE = re.compile(r"<(\S+)\+0x([0-9a-f]+)>")
+
+
+@lru_cache(maxsize=4)
+def _addressed(path: str) -> dict[str, list[tuple[int, str, int | None]]]:
+    """symbol -> [(address, instruction, branch target address or None)]."""
+    listing: dict[str, list[tuple[int, str, int | None]]] = {}
+    current, start = None, 0
+    for line in Path(path).read_text().splitlines():
+        header = re.match(r"^([0-9a-f]+) <(\S+)>:$", line)
+        if header:
+            start, current = int(header.group(1), 16), header.group(2)
+            listing[current] = []
+            continue
+        address = _ADDRESS_RE.search(line)
+        if current is None or not address:
+            continue
+        target = _TARGET_RE.search(line)
+        target_address = start + int(target.group(2), 16) if target and target.group(1) == current else None
+        listing[current].append((int(address.group(1), 16), line.split("//")[0].strip(), target_address))
+    return listing
+
+
+def loops(name: str, disassembly: Path | None = None) -> list[list[str]]:
+    """Instruction bodies of every backward branch of a kernel (target .. branch),
+    in listing order. The body with the most matrix instructions of a peak
+    kernel is its timed loop."""
+    path = disassembly or native_build.DISASSEMBLY
+    symbol = symbols(path)[name]
+    code = _addressed(str(path))[symbol]
+    bodies = []
+    for address, _text, target in code:
+        if target is not None and target <= address:
+            bodies.append([text for a, text, _ in code if target <= a <= address])
+    return bodies
+
+
+def hot_loop(name: str, disassembly: Path | None = None) -> list[str]:
+    """The loop body holding the most MFMA instructions (empty if none)."""
+    candidates = loops(name, disassembly)
+    best = max(candidates, key=lambda body: sum(mnemonic(l).startswith("v_mfma") for l in body), default=[])
+    return best if any(mnemonic(l).startswith("v_mfma") for l in best) else []
+
+
+def loop_summary(name: str, disassembly: Path | None = None) -> dict:
+    """What the timed loop issues: MFMA count and every other mnemonic with its count."""
+    body = hot_loop(name, disassembly)
+    counts: dict[str, int] = {}
+    for line in body:
+        counts[mnemonic(line)] = counts.get(mnemonic(line), 0) + 1
+    matrix = {k: v for k, v in counts.items() if k.startswith("v_mfma")}
+    other = {k: v for k, v in counts.items() if not k.startswith("v_mfma")}
+    vector_other = {k: v for k, v in other.items() if not k.startswith("s_")}
+    return {"timed_loop_matrix_instructions": sum(matrix.values()),
+            "timed_loop_matrix_types": sorted(matrix),
+            "timed_loop_other_instructions": other,
+            "timed_loop_vector_memory_or_alu": vector_other}
+
+
 def resources(name: str, build_dir: Path | None = None, disassembly: Path | None = None) -> dict:
     mapping = symbols(disassembly)
     metadata = _metadata(str(build_dir or native_build.BUILD)).get(mapping.get(name, ""), {})

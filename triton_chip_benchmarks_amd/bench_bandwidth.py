@@ -100,6 +100,17 @@ def check_read(src, sink, block_size):
             "reference_device": str(src.device)}
 
 
+def cache_regime(buffer_bytes, cache_bytes, quick):
+    """(regime, peak_eligible): a copy counts as an HBM rate only when each
+    buffer is at least 4x the last-level cache (bench_bandwidth.py:181-188)
+    and the run is not a smoke run. Unknown cache capacity is never eligible."""
+    if not cache_bytes:
+        return "unknown_l2", False
+    if buffer_bytes >= 4 * cache_bytes:
+        return "larger_than_l2", not quick
+    return "cache_sensitive", False
+
+
 def parse_args(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     add_common_arguments(parser)
@@ -184,9 +195,7 @@ def main(argv=None):
         required = (2 if "copy" in modes else 1) * buffer_bytes + max_sink
         if free_bytes is not None and required + 512 * 2**20 > free_bytes:
             raise SystemExit(f"Insufficient free GPU memory for {size_mib} MiB buffers; reduce --sizes-mib.")
-        regime = ("unknown_l2" if not cache_bytes else
-                  "larger_than_l2" if buffer_bytes >= 4 * cache_bytes else "cache_sensitive")
-        peak_eligible = regime == "larger_than_l2" and not args.quick
+        regime, peak_eligible = cache_regime(buffer_bytes, cache_bytes, args.quick)
         if not peak_eligible:
             reason = ("smoke mode" if args.quick else "cache capacity is unavailable" if not cache_bytes
                       else "buffer is smaller than 4x the last-level cache")

@@ -308,6 +308,7 @@ def compiled_info(kernel: str, dtype: str, input_precision: str | None) -> dict:
         info.update(audit.audit_tensor(audit.instructions(kernel), dtype, input_precision))
     except audit.TensorAuditError as exc:
         raise TensorUnsupportedError(str(exc)) from exc
+    info.update(audit.loop_summary(kernel))
     return info
 
 

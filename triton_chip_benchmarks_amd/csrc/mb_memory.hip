@@ -37,23 +37,31 @@ __device__ __forceinline__ void store_elem(T* ptr, T value) {
 template <typename T, int VPT, bool NT>
 __global__ void __launch_bounds__(1024) copy_kernel(const T* __restrict__ src, T* __restrict__ dst,
                                                      uint64_t n) {
-  const uint64_t threads = blockDim.x;
-  const uint64_t step = threads * VPT;
+  const uint32_t block_threads = blockDim.x;
+  const uint64_t step = static_cast<uint64_t>(block_threads) * VPT;
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * step;
   for (uint64_t base = blockIdx.x * step + threadIdx.x; base < n; base += stride) {
+    // Opaque per trip: otherwise the grid-stride loop keeps one 64-bit scalar
+    // pointer per vector and per operand live across trips, which exceeds the
+    // SGPR file at 16 vectors per lane and spills.
+    uint32_t threads = block_threads;
+    asm("" : "+s"(threads));
+    const T* s = src + base;
+    T* d = dst + base;
+    const uint64_t left = n - base;
     T values[VPT];
-    if (base + (VPT - 1) * threads < n) {
+    if (left > static_cast<uint64_t>(VPT - 1) * threads) {
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) values[j] = load_elem<T, NT>(src + base + j * threads);
+      for (int j = 0; j < VPT; ++j) values[j] = load_elem<T, NT>(s + j * threads);
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) store_elem<T, NT>(dst + base + j * threads, values[j]);
+      for (int j = 0; j < VPT; ++j) store_elem<T, NT>(d + j * threads, values[j]);
     } else {
 #pragma unroll
       for (int j = 0; j < VPT; ++j)
-        if (base + j * threads < n) values[j] = load_elem<T, NT>(src + base + j * threads);
+        if (j * threads < left) values[j] = load_elem<T, NT>(s + j * threads);
 #pragma unroll
       for (int j = 0; j < VPT; ++j)
-        if (base + j * threads < n) store_elem<T, NT>(dst + base + j * threads, values[j]);
+        if (j * threads < left) store_elem<T, NT>(d + j * threads, values[j]);
     }
   }
 }
