@@ -6,17 +6,26 @@ MI355X peak". One step is one pass of the hot path over resident synthetic
 inputs - one launch of each headline kernel:
   hbm_copy    mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from seed 0) into a
               second buffer (memory_bandwidth row);
-  peak_bf16   mb_tensor_peak BF16, 128x128x64 tiles, 2 chains, 1024 MFMA
-              iterations, 2 workgroups per CU (tensor_bf16 row);
-  peak_fp8    the same with FP8 E4M3, 128x128x128 tiles (tensor_fp8 row);
-  peak_mxfp4  the same with MX FP4 E2M1 + E8M0 scales, 128x128x256 tiles
-              (tensor_fp4 row).
+  peak_bf16   mb_tensor_peak BF16: the resident-operand variant that loops a
+              256x256x64 LDS tile 1024 times per workgroup, 2 workgroups per
+              CU (tensor_bf16 row);
+  peak_fp8    FP8 E4M3, 128x128x128 tiles, 2 chains, 1024 iterations, 4
+              workgroups per CU (tensor_fp8 row);
+  peak_mxfp4  MX FP4 E2M1 + E8M0 scales, 128x128x256 tiles, 2 chains, 1024
+              iterations, 4 workgroups per CU (tensor_fp4 row).
 Operands follow the reference's peak lattices (bench_tensor.py:614-672). Every
 kernel's output is validated before timing with the product's own checks
 (bit equality for the copy; exact float64 lattice references under the
-reference's tolerance for the MFMA rows). The K timed steps are bracketed by
-torch.cuda.synchronize(); per-kernel durations come from HIP events recorded
-around each launch on the launch stream.
+reference's tolerance for the MFMA rows).
+
+Timing: for each kernel in turn, W untimed warmup launches, then its K timed
+launches back to back between two torch.cuda.synchronize() calls, as the
+reference's batch timing does (common.py:295-534). MI355X raises its clock
+over ~40 ms when a matrix-bound kernel follows a memory-bound one, and the
+per-kernel warmup keeps that ramp out of the timed launches. A kernel's
+ms_per_launch is its batch time between two HIP events on the launch stream
+over K (no event between launches, as in the reference's event batches);
+ms_per_step is the sum of the kernels' batch times over K.
 
 value = mean over the headline rows of (achieved rate / MI355X published
 peak), in percent; the absolute rates are in "rows". The CPU baseline times
@@ -39,19 +48,23 @@ METRIC = "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of MI355X peak"
 COPY_ELEMENTS = 2**28
 COPY_SEED = 0
 # Launch shapes chosen from the bench_bandwidth / bench_tensor sweeps on MI355X.
-COPY_CONFIG = {"block_threads": 256, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": True}
+# One 64-lane wave per workgroup, one 16-byte vector per lane: the fastest measured
+# shape on MI355X (more vectors per lane or larger workgroups lose 1-8%).
+COPY_CONFIG = {"block_threads": 64, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": True}
 PEAK_ITERATIONS = 1024
-PEAK_BLOCKS_PER_CU = 2
-PEAK_TILES = {"bf16": (128, 128, 64), "fp8": (128, 128, 128), "fp4": (128, 128, 256)}
+# (tile M, N, K, chains, workgroups per CU). BF16 is BASELINE's resident
+# variant; FP8 and MXFP4 use the fastest tiles of the bench_tensor sweep.
+PEAK_SHAPES = {"bf16": (256, 256, 64, 1, 2), "fp8": (128, 128, 128, 2, 4), "fp4": (128, 128, 256, 2, 4)}
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_per_launch.txt"
-CPU_BUDGET_S = 4.0  # per row, so the default run stays within a few minutes
+CPU_ROW_BUDGET_S = 4.0  # host seconds per row: about 16 s of CPU work in all
 
 
 def parse_args(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=20,
+                        help="untimed launches of each kernel right before its timed ones (default: 20)")
     parser.add_argument("--no-cpu-baseline", action="store_true",
                         help="Skip the timed CPU baseline leg (it is on by default)")
     parser.add_argument("--rows", nargs="+", help="Subset of headline rows: hbm_copy peak_bf16 peak_fp8 peak_mxfp4")
@@ -127,7 +140,7 @@ class CopyWorkload:
         from oracle import memory
 
         sample = np.random.default_rng(COPY_SEED).uniform(-1, 1, size=2**26).astype(np.float32)
-        best = _best_of(lambda: memory.copy(sample), CPU_BUDGET_S / 4)
+        best = _best_of(lambda: memory.copy(sample), CPU_ROW_BUDGET_S)
         return 2 * sample.nbytes / best / 1e9, 1, "oracle.memory.copy (numpy) of 2^26 fp32 (256 MiB)"
 
 
@@ -136,15 +149,16 @@ class PeakWorkload:
 
     unit, bound = "TFLOP/s", "mfma"
 
-    def __init__(self, torch, dtype, blocks):
+    def __init__(self, torch, dtype, compute_units):
         from triton_chip_benchmarks_amd import _native, bench_tensor
 
         self.torch, self.bt, self.dtype = torch, bench_tensor, dtype
         self.name = "peak_mxfp4" if dtype == "fp4" else f"peak_{dtype}"
         self.metric_key = f"tensor_{dtype}"
-        m, n, k = PEAK_TILES[dtype]
+        m, n, k, chains, per_cu = PEAK_SHAPES[dtype]
+        blocks = per_cu * compute_units
         self.config = next(c for c in _native.peak_configs(dtype)
-                           if (c["tile_m"], c["tile_n"], c["tile_k"]) == (m, n, k) and c["chains"] == 2
+                           if (c["tile_m"], c["tile_n"], c["tile_k"]) == (m, n, k) and c["chains"] == chains
                            and not c["b_nk"])
         self.kernel = _native.peak_kernel_name(dtype, self.config)
         self.blocks = blocks
@@ -156,7 +170,7 @@ class PeakWorkload:
         self.work = 2 * m * n * k * PEAK_ITERATIONS * self.config["chains"] * blocks  # bench_tensor.py:1242
         self.dtype_label = {"bf16": "bf16", "fp8": "fp8_e4m3", "fp4": "mxfp4_e2m1"}[dtype]
         self.config_summary = {"tile": f"{m}x{n}x{k}", "chains": self.config["chains"], "blocks": blocks,
-                               "iterations": PEAK_ITERATIONS, "b_layout": "kn"}
+                               "blocks_per_cu": per_cu, "iterations": PEAK_ITERATIONS, "b_layout": "kn"}
 
     def launch(self):
         self.bt.launch_peak(self.dtype, self.config, self.a, self.b, self.c, PEAK_ITERATIONS, self.scales)
@@ -179,17 +193,17 @@ class PeakWorkload:
 
         from oracle import tensor as ot
 
-        m, n, k = PEAK_TILES[self.dtype]
+        m, n, k, chains, _ = PEAK_SHAPES[self.dtype]
         rng = np.random.default_rng(0)
         blocks = 64
         a = ot.ternary_lattice(rng, (blocks, m, k))
-        b = ot.ternary_lattice(rng, (2, blocks, k, n))
-        # One host iteration = both chains' tile products of every sampled block.
-        best = _best_of(lambda: ot.peak_reference(a, b, 1), CPU_BUDGET_S / 4)
-        flops = 2 * m * n * k * 2 * blocks
+        b = ot.ternary_lattice(rng, (chains, blocks, k, n))
+        # One host iteration = every chain's tile product of every sampled block.
+        best = _best_of(lambda: ot.peak_reference(a, b, 1), CPU_ROW_BUDGET_S)
+        flops = 2 * m * n * k * chains * blocks
         return flops / best / 1e12, _blas_threads(), (
-            f"oracle.tensor.peak_reference (numpy float64 matmul) of {blocks} blocks x 2 chains of "
-            f"{m}x{n}x{k} tiles, best repeat within {CPU_BUDGET_S / 4:g} s")
+            f"oracle.tensor.peak_reference (numpy float64 matmul) of {blocks} blocks x {chains} chain(s) of "
+            f"{m}x{n}x{k} tiles, best repeat within {CPU_ROW_BUDGET_S:g} s")
 
 
 def _blas_threads():
@@ -201,8 +215,8 @@ def _blas_threads():
         return os.cpu_count() or 1
 
 
-def build_workloads(torch, selected, blocks):
-    workloads = [CopyWorkload(torch)] + [PeakWorkload(torch, d, blocks) for d in ("bf16", "fp8", "fp4")]
+def build_workloads(torch, selected, compute_units):
+    workloads = [CopyWorkload(torch)] + [PeakWorkload(torch, d, compute_units) for d in ("bf16", "fp8", "fp4")]
     if selected:
         unknown = set(selected) - {w.name for w in workloads}
         if unknown:
@@ -228,37 +242,34 @@ def main(argv=None):
 
     require_gpu(0)
     info = _native.device_query(0)
-    blocks = PEAK_BLOCKS_PER_CU * info["compute_units"]
-    workloads = build_workloads(torch, args.rows, blocks)
+    workloads = build_workloads(torch, args.rows, info["compute_units"])
     checks = {w.name: w.validate() for w in workloads}
-    for _ in range(args.warmup):
-        for w in workloads:
-            w.launch()
-    torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(workloads) + 1)] for _ in range(args.steps)]
-    total_start, total_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    total_start.record(stream)
-    for step in range(args.steps):
-        events[step][0].record(stream)
-        for index, w in enumerate(workloads):
+    batch_ms = []
+    for w in workloads:
+        # W untimed warmup launches right before the kernel's K timed ones, so
+        # the clock has settled at this kernel's load when timing starts.
+        for _ in range(args.warmup):
             w.launch()
-            events[step][index + 1].record(stream)
-    total_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = total_start.elapsed_time(total_end)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            w.launch()
+        end.record(stream)
+        torch.cuda.synchronize()
+        batch_ms.append(start.elapsed_time(end))
+    total_ms = sum(batch_ms)
 
     traffic = traffic_table()
     rows = []
     for index, w in enumerate(workloads):
-        durations = [events[s][index].elapsed_time(events[s][index + 1]) for s in range(args.steps)]
-        average = sum(durations) / len(durations)
+        average = batch_ms[index] / args.steps
         achieved = w.rate(average)
         peak, _unit, basis = roofline.PEAKS[w.metric_key]
         rows.append({"row": w.metric_key, "name": w.name, "kernel": w.kernel, "value": achieved, "unit": w.unit,
-                     "ms_per_launch": average, "best_ms": min(durations), "peak": peak, "frac": achieved / peak,
+                     "ms_per_launch": average, "peak": peak, "frac": achieved / peak,
                      "peak_basis": basis, "bound": w.bound, "algorithmic_work_per_launch": w.work,
                      "work_unit": "bytes" if w.bound == "hbm" else "flop",
                      "traffic_bytes_per_launch": traffic.get(w.kernel),
@@ -290,8 +301,8 @@ def main(argv=None):
         "dtype": ",".join(getattr(w, "dtype_label", w.dtype) for w in workloads),
         "data": "synthetic: seeded uniform fp32 copy source; exact-lattice MFMA operands, resident in HBM",
         "config": {"workload": " + ".join(w.name for w in workloads), "device": info["name"], "arch": info["arch"],
-                   "compute_units": info["compute_units"], "peak_blocks": blocks,
-                   "peak_iterations": PEAK_ITERATIONS, "copy_elements": COPY_ELEMENTS},
+                   "compute_units": info["compute_units"], "peak_iterations": PEAK_ITERATIONS,
+                   "copy_elements": COPY_ELEMENTS, "timing": "K back-to-back launches per kernel, HIP events"},
         "roofline": roofline_block, "cpu_baseline": cpu, "rows": rows,
     }
     print(json.dumps(line))

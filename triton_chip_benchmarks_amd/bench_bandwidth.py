@@ -119,10 +119,10 @@ def parse_args(argv=None):
     parser.add_argument("--sizes-mib", type=positive_int, nargs="+", default=[256, 512, 1024, 2048],
                         help="Size of EACH source/destination buffer in MiB")
     parser.add_argument("--dtype", choices=["fp16", "bf16", "fp32"], default="fp32")
-    parser.add_argument("--block-sizes", type=positive_int, nargs="+", default=[1024, 4096, 16384],
+    parser.add_argument("--block-sizes", type=positive_int, nargs="+", default=[256, 1024, 4096, 16384],
                         help="Elements per workgroup step (copy) or per block sum (read)")
     parser.add_argument("--num-warps", type=positive_int, nargs="+",
-                        help="64-lane waves per workgroup (default: 4 8)")
+                        help="64-lane waves per workgroup (default: 1 4 8)")
     parser.add_argument("--nontemporal", choices=("off", "on", "both"), default="both",
                         help="Copy with streaming (nt) loads/stores (default: measure both)")
     parser.add_argument("--grid-blocks", type=int, default=0,
@@ -143,7 +143,7 @@ def parse_args(argv=None):
 
 
 def configurations(args, element_size):
-    warps = args.num_warps or ([4] if args.quick else [4, 8])
+    warps = args.num_warps or ([4] if args.quick else [1, 4, 8])
     nontemporal = {"off": [False], "on": [True], "both": [False, True]}[args.nontemporal]
     configs = []
     for block in args.block_sizes:
