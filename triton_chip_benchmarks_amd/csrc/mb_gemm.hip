@@ -21,6 +21,12 @@
 //     i/8-th tile of XCD i%8's contiguous share, and within that share tiles
 //     are walked in GROUP_M-row bands, keeping A and B panels hot in the XCD's L2;
 //   * CHECKED instantiations bound every load and store for ragged shapes.
+//
+// 256x256 tiles of the 8- and 16-bit formats use gemm_dma_kernel instead when
+// the shape divides the tile: 8 waves (2 per SIMD), operands fed straight from
+// L2 into LDS by buffer_load_dwordx4 ... lds (no VGPR staging, no ds_write),
+// XOR-swizzled LDS rows (conflict-free ds_read_b128 without padding), and
+// fragment reads of substep s+1 issued ahead of the MFMAs of substep s.
 #include "mb_internal.h"
 #include "mb_mfma.h"
 
@@ -202,6 +208,160 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
       }
 }
 
+// ---- DMA-fed 256x256 kernel ------------------------------------------------
+
+// One 16-byte-per-lane LDS DMA: lane l's 16 bytes land at lds_addr + 16 * l.
+// Issued as inline assembly so the compiler's wait-count pass does not force a
+// full vmcnt(0) before every LDS read; the kernel waits explicitly instead.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, uint32_t lds_addr) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory");
+}
+
+__device__ __forceinline__ void wait_all_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Word 3 of a gfx9 buffer resource: 32-bit data format, no swizzle, raw offsets.
+constexpr int kBufferWord3 = 0x00020000;
+
+// C = A . B^T for M, N multiples of 256 and K * bits multiples of ROWB * 8;
+// A, B byte offsets must fit in 31 bits. Each K step stages a 256 x ROWB-byte
+// slice of A and of B (one LDS stage, double-buffered). LDS row r holds its
+// 16-byte chunk c at position c ^ ((r / (256 / ROWB)) % (ROWB / 16)): any 16
+// consecutive rows read at one logical chunk hit 16 distinct bank groups.
+template <class Op, int ROWB, int WAVES_M, int WAVES_N>
+__global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
+    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, typename Op::Out* __restrict__ C,
+                    int M, int N, int K, int group_m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 256, BN = 256;
+  constexpr int NW = WAVES_M * WAVES_N;
+  constexpr int CPR = ROWB / 16;      // 16-byte chunks per LDS row
+  constexpr int RPI = 1024 / ROWB;    // rows one DMA instruction fills (64 lanes x 16 bytes)
+  constexpr int RPB = 256 / ROWB;     // rows per 256 bytes: the swizzle period
+  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int INSTR = (BM + BN) / RPI / NW;  // DMA instructions per wave per K step
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / Op::M, TN = WN / Op::N;
+  constexpr int KB = MfmaGeometry<Op>::K_BYTES, KSTEPS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
+  static_assert((BM / RPI) % NW == 0, "an instruction's rows are all A or all B, whatever the wave");
+  static_assert(ROWB % KB == 0 && Op::LANE_BYTES % 16 == 0 && Op::M == 32, "whole 32x32 instructions per step");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+  // The array is otherwise written only by DMA, which the optimizer does not
+  // see as a store; one plain (never executed) store keeps its reads live.
+  if (K < 0) lds[threadIdx.x] = 0;
+
+  const int tiles_m = M / BM, tiles_n = N / BN;
+  const int count = gridDim.x;
+  int pid = blockIdx.x;
+  if (count % kXcds == 0) pid = (pid % kXcds) * (count / kXcds) + pid / kXcds;
+  const int band = group_m * tiles_n;
+  const int first_m = (pid / band) * group_m;
+  const int rows_in_band = min(tiles_m - first_m, group_m);
+  const int tile_m = first_m + (pid % band) % rows_in_band;
+  const int tile_n = (pid % band) / rows_in_band;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int row_bytes = K * Op::ELEM_BITS / 8;
+  const int k_steps = row_bytes / ROWB;
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Each resource covers exactly this tile's 256 rows of its operand.
+  const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(A + static_cast<int64_t>(m0) * row_bytes), (short)0, BM * row_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(B + static_cast<int64_t>(n0) * row_bytes), (short)0, BN * row_bytes, kBufferWord3);
+  const uint32_t lds_base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds)));
+  // DMA instruction j of this wave fills LDS rows rb*RPI .. rb*RPI+RPI-1 of the
+  // A|B stage, rb = j*NW + wave; lane l supplies row rb*RPI + l/CPR, physical
+  // chunk l%CPR, i.e. the global chunk that swizzles there.
+  int voff[INSTR];
+#pragma unroll
+  for (int j = 0; j < INSTR; ++j) {
+    const int row = (j * NW + wave) * RPI + lane / CPR;
+    const int chunk = (lane % CPR) ^ ((row / RPB) % CPR);
+    voff[j] = (row < BM ? row : row - BM) * row_bytes + chunk * 16;
+  }
+  auto issue = [&](int kt) {
+    const uint32_t stage = lds_base + (kt & 1) * STAGE;
+#pragma unroll
+    for (int j = 0; j < INSTR; ++j) {
+      const uint32_t dst = stage + (j * NW + wave) * 1024;
+      if (j * NW < BM / RPI) dma16(rsrc_a, voff[j], kt * ROWB, dst);
+      else dma16(rsrc_b, voff[j], kt * ROWB, dst);
+    }
+  };
+
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int lrow = lane & 31, lgroup = lane >> 5;
+  typename Op::Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = typename Op::Acc{};
+
+  // Fragment of LDS row `row` for substep ks: LANE_BYTES from logical chunks
+  // ks*KB/16 + lgroup*PIECES + p.
+  auto read = [&](const uint8_t* stage, int row, int ks) {
+    i32x4 parts[PIECES];
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) {
+      const int c = ks * (KB / 16) + lgroup * PIECES + p;
+      parts[p] = *reinterpret_cast<const i32x4*>(stage + row * ROWB + ((c ^ ((row / RPB) % CPR)) * 16));
+    }
+    if constexpr (PIECES == 1) {
+      return __builtin_bit_cast(typename Op::Frag, parts[0]);
+    } else {
+      return typename Op::Frag{parts[0][0], parts[0][1], parts[0][2], parts[0][3],
+                               parts[1][0], parts[1][1], parts[1][2], parts[1][3]};
+    }
+  };
+
+  issue(0);
+  for (int kt = 0; kt < k_steps; ++kt) {
+    // Step kt's DMA is complete for this wave; the barrier makes every wave's
+    // part visible and ends all reads of the other stage, which the next DMA
+    // then overwrites.
+    wait_all_dma();
+    __syncthreads();
+    if (kt + 1 < k_steps) issue(kt + 1);
+    const uint8_t* stage = lds + (kt & 1) * STAGE;
+    typename Op::Frag fa[2][TM], fb[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[0][i] = read(stage, wm * WM + i * 32 + lrow, 0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[0][j] = read(stage, BM + wn * WN + j * 32 + lrow, 0);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KSTEPS) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[cur ^ 1][i] = read(stage, wm * WM + i * 32 + lrow, ks + 1);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[cur ^ 1][j] = read(stage, BM + wn * WN + j * 32 + lrow, ks + 1);
+      }
+      // Keep the next substep's reads ahead of this substep's MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Op::mma(fa[cur][i], fb[cur][j], acc[i][j], 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < Op::ACC_REGS; ++r) {
+        const int row = m0 + wm * WM + i * 32 + Op::out_row(lane, r);
+        const int col = n0 + wn * WN + j * 32 + lrow;
+        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+      }
+#endif
+}
+
 using GemmLauncher = void (*)(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, void*, int, int, int,
                               int, uint32_t, hipStream_t);
 
@@ -212,6 +372,16 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
+template <class Op, int ROWB, int WM, int WN>
+void launch_gemm_dma(const uint8_t* a, const uint8_t* b, const uint8_t*, const uint8_t*, void* c, int m, int n, int k,
+                     int group_m, uint32_t blocks, hipStream_t stream) {
+  gemm_dma_kernel<Op, ROWB, WM, WN><<<dim3(blocks), dim3(64 * WM * WN), 0, stream>>>(
+      a, b, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+}
+
+// launch: shapes that divide the tile (nullptr: none, use launch_checked);
+// launch_checked: any shape. dma_row_bytes > 0 marks a DMA kernel, whose K
+// step is that many bytes and whose operand offsets must fit in 31 bits.
 struct GemmVariant {
   int format;
   mb_gemm_config config;
@@ -221,6 +391,7 @@ struct GemmVariant {
   GemmLauncher launch_checked;
   int out_bytes;
   int elem_bits;
+  int dma_row_bytes;
 };
 
 #define MB_GEMM(FMT, OP, BM, BN, BK, WM, WN, NAME)                                                           \
@@ -231,19 +402,33 @@ struct GemmVariant {
               launch_gemm<OP, BM, BN, BK, WM, WN, false>,                                                    \
               launch_gemm<OP, BM, BN, BK, WM, WN, true>,                                                     \
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
-              OP::ELEM_BITS}
+              OP::ELEM_BITS,                                                                                 \
+              0}
+
+// 256x256 tile: the DMA kernel (8 waves, 128-byte K steps) for exact shapes,
+// the LDS-staged checked kernel for ragged ones.
+#define MB_GEMM_DMA(FMT, OP, BK, NAME)                                                                       \
+  GemmVariant{FMT,                                                                                           \
+              mb_gemm_config{256, 256, BK, 512},                                                             \
+              NAME,                                                                                          \
+              reinterpret_cast<const void*>(gemm_dma_kernel<OP, 128, 2, 4>),                                 \
+              launch_gemm_dma<OP, 128, 2, 4>,                                                                \
+              launch_gemm<OP, 256, 256, BK, 2, 2, true>,                                                     \
+              static_cast<int>(sizeof(typename OP::Out)),                                                    \
+              OP::ELEM_BITS,                                                                                 \
+              128}
 
 const GemmVariant kGemmVariants[] = {
-    MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 256, 64, 2, 2, "gemm_bf16_256x256x64"),
+    MB_GEMM_DMA(MB_MATRIX_BF16, MfmaBf16, 64, "gemm_bf16_256x256x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
-    MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 256, 64, 2, 2, "gemm_f16_256x256x64"),
+    MB_GEMM_DMA(MB_MATRIX_F16, MfmaF16, 64, "gemm_f16_256x256x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 256, 128, 2, 2, "gemm_fp8_256x256x128"),
+    MB_GEMM_DMA(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, "gemm_fp8_256x256x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
-    MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 256, 128, 2, 2, "gemm_i8_256x256x128"),
+    MB_GEMM_DMA(MB_MATRIX_I8, MfmaI8, 128, "gemm_i8_256x256x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
@@ -329,8 +514,11 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
   const uint64_t tiles = static_cast<uint64_t>((m + v.tile_m - 1) / v.tile_m) * ((n + v.tile_n - 1) / v.tile_n);
   if (tiles > 0x7fffffffull) return fail(MB_ERR_INVALID, "mb_gemm: too many tiles");
   const bool exact = m % v.tile_m == 0 && n % v.tile_n == 0 && k % v.tile_k == 0;
+  // The DMA kernel addresses each tile's 256 operand rows with 32-bit offsets.
+  const bool offsets_fit = variant->dma_row_bytes == 0 ||
+                           (row_bytes % variant->dma_row_bytes == 0 && 256 * row_bytes <= 0x7fffffffull);
   const int group = group_m ? static_cast<int>(group_m) : 8;
-  GemmLauncher launch = exact ? variant->launch : variant->launch_checked;
+  GemmLauncher launch = exact && offsets_fit ? variant->launch : variant->launch_checked;
   launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
          static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), group,
          static_cast<uint32_t>(tiles), static_cast<hipStream_t>(stream));
