@@ -119,3 +119,36 @@ def test_gemm_baseline_size_checksums(gpu, dtype, size):
         assert np.array_equal(got[rows], sampled)
         assert np.array_equal(got.sum(axis=0), column_sums)
         assert np.array_equal(got.sum(axis=1), row_sums)
+
+
+def test_mxfp4_gemm_applies_each_rows_group_scale(gpu):
+    """E8M0 scales drawn from {126, 127, 128} per (row, 32-element group): a
+    wrong row or group index, or a scale applied to the wrong operand, moves
+    the result off the exact oracle. Products are multiples of 2^-4 below 145
+    and K <= 1024, so every partial sum is exact in fp32 in any order."""
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+
+    rng = np.random.default_rng(11)
+    for config in _configs("fp4"):
+        shapes = [(config["tile_m"], config["tile_n"], 2 * config["tile_k"]),
+                  (2 * config["tile_m"], config["tile_n"], 4 * config["tile_k"]),
+                  (config["tile_m"] + 37, config["tile_n"] - 5, 160)]
+        for m, n, k in shapes:
+            print(f"gemm fp4 scaled tile {config['tile_m']}x{config['tile_n']}x{config['tile_k']} shape {m}x{n}x{k}",
+                  flush=True)
+            codes_a = rng.integers(0, 16, (m, k), dtype=np.uint8)
+            codes_b = rng.integers(0, 16, (n, k), dtype=np.uint8)
+            sa = rng.integers(126, 129, (m, k // 32), dtype=np.uint8)
+            sb = rng.integers(126, 129, (n, k // 32), dtype=np.uint8)
+            c = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+            _native.gemm("fp4", config, torch.from_numpy(ot.pack_e2m1(codes_a)).cuda(),
+                         torch.from_numpy(ot.pack_e2m1(codes_b)).cuda(), c, m, n, k,
+                         torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda())
+            torch.cuda.synchronize()
+            a_values = ot.e2m1_decode(codes_a) * np.repeat(ot.e8m0_decode(sa), 32, axis=1)
+            b_values = ot.e2m1_decode(codes_b) * np.repeat(ot.e8m0_decode(sb), 32, axis=1)
+            expected = ot.gemm_reference(a_values, b_values.T)
+            got = c.cpu().numpy().astype(np.float64)
+            assert np.array_equal(got, expected), f"max error {np.abs(got - expected).max()}"

@@ -219,6 +219,13 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int voffset, 
                : "memory");
 }
 
+// One 4-byte-per-lane LDS DMA (E8M0 scale rows): lane l's 4 bytes land at lds_addr + 4 * l.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, uint32_t lds_addr) {
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory");
+}
+
 __device__ __forceinline__ void wait_all_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Word 3 of a gfx9 buffer resource: 32-bit data format, no swizzle, raw offsets.
@@ -226,25 +233,32 @@ constexpr int kBufferWord3 = 0x00020000;
 
 // C = A . B^T for M, N multiples of 256 and K * bits multiples of ROWB * 8;
 // A, B byte offsets must fit in 31 bits. Each K step stages a 256 x ROWB-byte
-// slice of A and of B (one LDS stage, double-buffered). LDS row r holds its
+// slice of A and of B (one LDS stage, double-buffered); for MXFP4 the stage
+// also holds the step's E8M0 scales, 256 rows x ROWB/16 bytes for A and for B. LDS row r holds its
 // 16-byte chunk c at position c ^ ((r / (256 / ROWB)) % (ROWB / 16)): any 16
 // consecutive rows read at one logical chunk hit 16 distinct bank groups.
 template <class Op, int ROWB, int WAVES_M, int WAVES_N>
 __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
-    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, typename Op::Out* __restrict__ C,
-                    int M, int N, int K, int group_m) {
+    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__ SA,
+                    const uint8_t* __restrict__ SB, typename Op::Out* __restrict__ C, int M, int N, int K,
+                    int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 256, BN = 256;
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int CPR = ROWB / 16;      // 16-byte chunks per LDS row
   constexpr int RPI = 1024 / ROWB;    // rows one DMA instruction fills (64 lanes x 16 bytes)
   constexpr int RPB = 256 / ROWB;     // rows per 256 bytes: the swizzle period
-  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int DATA = (BM + BN) * ROWB;
+  // MXFP4: ROWB bytes hold 2*ROWB E2M1 codes, i.e. ROWB/16 scale bytes per row.
+  constexpr int SCALE_ROW = Op::SCALED ? ROWB / 16 : 0;
+  constexpr int STAGE = DATA + (BM + BN) * SCALE_ROW;
   constexpr int INSTR = (BM + BN) / RPI / NW;  // DMA instructions per wave per K step
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / Op::M, TN = WN / Op::N;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES, KSTEPS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
   static_assert((BM / RPI) % NW == 0, "an instruction's rows are all A or all B, whatever the wave");
   static_assert(ROWB % KB == 0 && Op::LANE_BYTES % 16 == 0 && Op::M == 32, "whole 32x32 instructions per step");
+  static_assert(!Op::SCALED || (SCALE_ROW == 8 && (BM + BN) * SCALE_ROW / 256 == 2 * NW),
+                "scale DMA: one 4-byte-lane instruction of A rows and one of B rows per wave");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
   // The array is otherwise written only by DMA, which the optimizer does not
   // see as a store; one plain (never executed) store keeps its reads live.
@@ -281,6 +295,18 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
     const int chunk = (lane % CPR) ^ ((row / RPB) % CPR);
     voff[j] = (row < BM ? row : row - BM) * row_bytes + chunk * 16;
   }
+  // MXFP4 scales: wave w moves A scale rows 32w .. 32w+31 and the same B
+  // rows; lane l carries half l%2 of row 32w + l/2's SCALE_ROW bytes.
+  const int scale_cols = Op::SCALED ? K / 32 : 0;
+  __amdgpu_buffer_rsrc_t rsrc_sa = rsrc_a, rsrc_sb = rsrc_b;
+  int scale_voff = 0;
+  if constexpr (Op::SCALED) {
+    rsrc_sa = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SA + static_cast<int64_t>(m0) * scale_cols),
+                                                (short)0, BM * scale_cols, kBufferWord3);
+    rsrc_sb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SB + static_cast<int64_t>(n0) * scale_cols),
+                                                (short)0, BN * scale_cols, kBufferWord3);
+    scale_voff = (wave * 32 + lane / 2) * scale_cols + (lane % 2) * 4;
+  }
   auto issue = [&](int kt) {
     const uint32_t stage = lds_base + (kt & 1) * STAGE;
 #pragma unroll
@@ -288,6 +314,10 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
       const uint32_t dst = stage + (j * NW + wave) * 1024;
       if (j * NW < BM / RPI) dma16(rsrc_a, voff[j], kt * ROWB, dst);
       else dma16(rsrc_b, voff[j], kt * ROWB, dst);
+    }
+    if constexpr (Op::SCALED) {
+      dma4(rsrc_sa, scale_voff, kt * SCALE_ROW, stage + DATA + wave * 256);
+      dma4(rsrc_sb, scale_voff, kt * SCALE_ROW, stage + DATA + BM * SCALE_ROW + wave * 256);
     }
   };
 
@@ -325,6 +355,20 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
     __syncthreads();
     if (kt + 1 < k_steps) issue(kt + 1);
     const uint8_t* stage = lds + (kt & 1) * STAGE;
+    // MXFP4: a lane's scale for substep ks is group 2*ks + lgroup of its row;
+    // after shifting the row's 8 bytes by 8*lgroup, it is byte 2*ks, i.e. byte
+    // 0 of the value shifted by 16*ks (the instruction reads byte 0).
+    uint64_t srow_a[TM], srow_b[TN];
+    if constexpr (Op::SCALED) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        srow_a[i] = *reinterpret_cast<const uint64_t*>(stage + DATA + (wm * WM + i * 32 + lrow) * SCALE_ROW) >>
+                    (8 * lgroup);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        srow_b[j] = *reinterpret_cast<const uint64_t*>(stage + DATA + (BM + wn * WN + j * 32 + lrow) * SCALE_ROW) >>
+                    (8 * lgroup);
+    }
     typename Op::Frag fa[2][TM], fb[2][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa[0][i] = read(stage, wm * WM + i * 32 + lrow, 0);
@@ -344,7 +388,14 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = Op::mma(fa[cur][i], fb[cur][j], acc[i][j], 0, 0);
+        for (int j = 0; j < TN; ++j) {
+          int scale_a = 0, scale_b = 0;
+          if constexpr (Op::SCALED) {
+            scale_a = static_cast<int>(srow_a[i] >> (16 * ks));
+            scale_b = static_cast<int>(srow_b[j] >> (16 * ks));
+          }
+          acc[i][j] = Op::mma(fa[cur][i], fb[cur][j], acc[i][j], scale_a, scale_b);
+        }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -362,21 +413,26 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
 #endif
 }
 
+// Launchers size their own grid: one workgroup per output tile of their kernel.
 using GemmLauncher = void (*)(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, void*, int, int, int,
-                              int, uint32_t, hipStream_t);
+                              int, hipStream_t);
+
+inline uint32_t tile_count(int m, int n, int bm, int bn) {
+  return static_cast<uint32_t>(((m + bm - 1) / bm) * static_cast<int64_t>((n + bn - 1) / bn));
+}
 
 template <class Op, int BM, int BN, int BK, int WM, int WN, bool CHECKED>
 void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m, int n,
-                 int k, int group_m, uint32_t blocks, hipStream_t stream) {
-  gemm_kernel<Op, BM, BN, BK, WM, WN, CHECKED><<<dim3(blocks), dim3(64 * WM * WN), 0, stream>>>(
+                 int k, int group_m, hipStream_t stream) {
+  gemm_kernel<Op, BM, BN, BK, WM, WN, CHECKED><<<dim3(tile_count(m, n, BM, BN)), dim3(64 * WM * WN), 0, stream>>>(
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
 template <class Op, int ROWB, int WM, int WN>
-void launch_gemm_dma(const uint8_t* a, const uint8_t* b, const uint8_t*, const uint8_t*, void* c, int m, int n, int k,
-                     int group_m, uint32_t blocks, hipStream_t stream) {
-  gemm_dma_kernel<Op, ROWB, WM, WN><<<dim3(blocks), dim3(64 * WM * WN), 0, stream>>>(
-      a, b, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+void launch_gemm_dma(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m, int n,
+                     int k, int group_m, hipStream_t stream) {
+  gemm_dma_kernel<Op, ROWB, WM, WN><<<dim3(tile_count(m, n, 256, 256)), dim3(64 * WM * WN), 0, stream>>>(
+      a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
 // launch: shapes that divide the tile (nullptr: none, use launch_checked);
@@ -406,31 +462,32 @@ struct GemmVariant {
               0}
 
 // 256x256 tile: the DMA kernel (8 waves, 128-byte K steps) for exact shapes,
-// the LDS-staged checked kernel for ragged ones.
-#define MB_GEMM_DMA(FMT, OP, BK, NAME)                                                                       \
+// a checked LDS-staged kernel (tile CM x CN) for ragged ones.
+#define MB_GEMM_DMA(FMT, OP, BK, CM, CN, NAME)                                                               \
   GemmVariant{FMT,                                                                                           \
               mb_gemm_config{256, 256, BK, 512},                                                             \
               NAME,                                                                                          \
               reinterpret_cast<const void*>(gemm_dma_kernel<OP, 128, 2, 4>),                                 \
               launch_gemm_dma<OP, 128, 2, 4>,                                                                \
-              launch_gemm<OP, 256, 256, BK, 2, 2, true>,                                                     \
+              launch_gemm<OP, CM, CN, BK, 2, 2, true>,                                                       \
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
               OP::ELEM_BITS,                                                                                 \
               128}
 
 const GemmVariant kGemmVariants[] = {
-    MB_GEMM_DMA(MB_MATRIX_BF16, MfmaBf16, 64, "gemm_bf16_256x256x64"),
+    MB_GEMM_DMA(MB_MATRIX_BF16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
-    MB_GEMM_DMA(MB_MATRIX_F16, MfmaF16, 64, "gemm_f16_256x256x64"),
+    MB_GEMM_DMA(MB_MATRIX_F16, MfmaF16, 64, 256, 256, "gemm_f16_256x256x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM_DMA(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, "gemm_fp8_256x256x128"),
+    MB_GEMM_DMA(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
-    MB_GEMM_DMA(MB_MATRIX_I8, MfmaI8, 128, "gemm_i8_256x256x128"),
+    MB_GEMM_DMA(MB_MATRIX_I8, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
+    MB_GEMM_DMA(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 128, "gemm_mxfp4_256x256x256"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, "gemm_mxfp4_128x128x256"),
     MB_GEMM(MB_MATRIX_F64, MfmaF64, 128, 128, 16, 2, 2, "gemm_f64_128x128x16"),
@@ -511,17 +568,21 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
       return fail(MB_ERR_INVALID, "mb_gemm: scale buffers too small ([M|N][K/32] bytes needed)");
   }
   const mb_gemm_config& v = variant->config;
-  const uint64_t tiles = static_cast<uint64_t>((m + v.tile_m - 1) / v.tile_m) * ((n + v.tile_n - 1) / v.tile_n);
-  if (tiles > 0x7fffffffull) return fail(MB_ERR_INVALID, "mb_gemm: too many tiles");
   const bool exact = m % v.tile_m == 0 && n % v.tile_n == 0 && k % v.tile_k == 0;
   // The DMA kernel addresses each tile's 256 operand rows with 32-bit offsets.
-  const bool offsets_fit = variant->dma_row_bytes == 0 ||
-                           (row_bytes % variant->dma_row_bytes == 0 && 256 * row_bytes <= 0x7fffffffull);
+  // Its scale rows are moved 4 bytes per lane, so they must be 4-byte aligned.
+  const bool offsets_fit =
+      variant->dma_row_bytes == 0 ||
+      (row_bytes % variant->dma_row_bytes == 0 && 256 * row_bytes <= 0x7fffffffull &&
+       (format != MB_MATRIX_MXFP4 || (aligned(scale_a, 4) && aligned(scale_b, 4))));
+  // The tile count of the smallest tile any launcher uses bounds the grid.
+  const uint64_t max_tiles = static_cast<uint64_t>((m + 63) / 64) * ((n + 63) / 64);
+  if (max_tiles > 0x7fffffffull) return fail(MB_ERR_INVALID, "mb_gemm: too many tiles");
   const int group = group_m ? static_cast<int>(group_m) : 8;
   GemmLauncher launch = exact && offsets_fit ? variant->launch : variant->launch_checked;
   launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
          static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), group,
-         static_cast<uint32_t>(tiles), static_cast<hipStream_t>(stream));
+         static_cast<hipStream_t>(stream));
   return launch_status(variant->name);
 }
 
