@@ -49,8 +49,9 @@ COPY_ELEMENTS = 2**28
 COPY_SEED = 0
 # Launch shapes chosen from the bench_bandwidth / bench_tensor sweeps on MI355X.
 # One 64-lane wave per workgroup, one 16-byte vector per lane: the fastest measured
-# shape on MI355X (more vectors per lane or larger workgroups lose 1-8%).
-COPY_CONFIG = {"block_threads": 64, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": True}
+# shape on MI355X (more vectors per lane or larger workgroups lose 1-8%); streaming
+# policy: nt loads, device-scope stores written through the L2 (~1% over nt stores).
+COPY_CONFIG = {"block_threads": 64, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": "stream"}
 PEAK_ITERATIONS = 1024
 # (tile M, N, K, chains, workgroups per CU). BF16 is BASELINE's resident
 # variant; FP8 and MXFP4 use the fastest tiles of the bench_tensor sweep.
@@ -114,8 +115,8 @@ class CopyWorkload:
         self.src = torch.empty(COPY_ELEMENTS, device="cuda", dtype=torch.float32).uniform_(-1, 1, generator=generator)
         self.dst = torch.empty_like(self.src)
         self.work = 2 * self.src.numel() * 4  # algorithmic bytes: read + write (bench_bandwidth.py:212)
-        self.kernel = f"copy_dwordx4_vpt{COPY_CONFIG['vectors_per_thread']}" + (
-            "_nt" if COPY_CONFIG["nontemporal"] else "")
+        self.kernel = f"copy_dwordx4_vpt{COPY_CONFIG['vectors_per_thread']}" + bench_bandwidth.POLICY_SUFFIX[
+            bench_bandwidth.copy_policy(COPY_CONFIG["nontemporal"])]
         self.config = {"elements": COPY_ELEMENTS, "dtype": "fp32", **COPY_CONFIG}
 
     def launch(self):

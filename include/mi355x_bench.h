@@ -81,7 +81,8 @@ int mb_kernel_attributes_query(const char* name, mb_kernel_attributes* out);
 /* ---- memory: copy and read ---------------------------------------------- */
 
 /* Flags for mb_copy. */
-#define MB_COPY_NONTEMPORAL 1u /* streaming (nt) loads and stores */
+#define MB_COPY_NONTEMPORAL 1u   /* streaming (nt) loads; nt stores unless MB_COPY_WRITE_THROUGH */
+#define MB_COPY_WRITE_THROUGH 2u /* device-scope (sc1) stores, written through the XCD's L2 */
 
 /* dst[0:bytes) = src[0:bytes): a coalesced 16-byte-per-lane copy.
  * `block_threads` is a multiple of 64 up to 1024; each workgroup moves

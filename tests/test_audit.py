@@ -98,7 +98,10 @@ def test_registered_names_follow_the_mangled_template_arguments():
     assert audit.registered_name(symbol) == "tensor_peak_bf16_128x128x64_c2_kn"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_111gemm_kernelINS_9MfmaMxfp4ELi128ELi128ELi256ELi2ELi2ELb1EEEv") \
         == "gemm_mxfp4_128x128x256_checked"
-    assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIDv4_jLi1ELb1EEEv") == "copy_dwordx4_vpt1_nt"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIDv4_jLi1ELi1EEEv") == "copy_dwordx4_vpt1_nt"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIjLi8ELi2EEEv") == "copy_dword_vpt8_stream"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_9MfmaMxfp4ELi128ELi2ELi4EEEv") \
+        == "gemm_mxfp4_256x256x256"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
     assert audit.registered_name("unrelated_symbol") is None
 
@@ -156,6 +159,17 @@ def test_no_kernel_spills_or_uses_scratch(listing):
         info = audit.resources(name)
         assert info["register_spills"] == 0, (name, info)
         assert not info["scratch_bytes"], (name, info)
+
+
+def test_copy_policies_issue_their_cache_bits(listing):
+    for name, load_bits, store_bits in (("copy_dwordx4_vpt1", "", ""), ("copy_dwordx4_vpt1_nt", "nt", "nt"),
+                                        ("copy_dwordx4_vpt1_stream", "nt", "sc1")):
+        lines = audit.instructions(name)
+        loads = [l for l in lines if audit.mnemonic(l) == "global_load_dwordx4"]
+        stores = [l for l in lines if audit.mnemonic(l) == "global_store_dwordx4"]
+        assert loads and stores, name
+        assert all(l.split()[-1] == (load_bits or "off") for l in loads), (name, loads)
+        assert all(l.split()[-1] == (store_bits or "off") for l in stores), (name, stores)
 
 
 def test_no_packed_fp32_valu_anywhere():

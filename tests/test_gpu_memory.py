@@ -25,7 +25,7 @@ def _bits(tensor):
 
 
 @pytest.mark.parametrize("elements", [1, 3, 63, 64, 1000, 4096 + 17, (1 << 20) + 5])
-@pytest.mark.parametrize("vpt,nontemporal", [(1, False), (4, True), (16, False)])
+@pytest.mark.parametrize("vpt,nontemporal", [(1, False), (4, True), (16, False), (1, "stream"), (8, "stream")])
 def test_copy_ragged_sizes_bit_exact(gpu, elements, vpt, nontemporal):
     import torch
 
@@ -39,17 +39,18 @@ def test_copy_ragged_sizes_bit_exact(gpu, elements, vpt, nontemporal):
     assert (_bits(dst) == _bits(torch.from_numpy(memory.copy(src.cpu().numpy())))).all()
 
 
+@pytest.mark.parametrize("flags", [0, 3])
 @pytest.mark.parametrize("offset_bytes", [4, 1, 3])
-def test_copy_misaligned_pointers_take_narrow_accesses(gpu, offset_bytes):
+def test_copy_misaligned_pointers_take_narrow_accesses(gpu, offset_bytes, flags):
     import torch
 
     from triton_chip_benchmarks_amd import _native
 
-    print(f"misaligned copy offset={offset_bytes}", flush=True)
+    print(f"misaligned copy offset={offset_bytes} flags={flags}", flush=True)
     raw = torch.randint(0, 256, (1 << 16,), dtype=torch.uint8, device="cuda")
     out = torch.zeros_like(raw)
     count = (1 << 16) - 64
-    _native.call("mb_copy", raw.data_ptr() + offset_bytes, out.data_ptr() + offset_bytes, count, 256, 2, 0, 0,
+    _native.call("mb_copy", raw.data_ptr() + offset_bytes, out.data_ptr() + offset_bytes, count, 256, 2, 0, flags,
                  _native.stream_handle())
     torch.cuda.synchronize()
     got, want = out.cpu().numpy(), raw.cpu().numpy()

@@ -60,6 +60,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert library.mb_copy(1 << 20, 2 << 20, 64, 256, 3, 0, 0, None) == _native.MB_ERR_INVALID
     assert library.mb_copy(1 << 20, (1 << 20) + 16, 64, 256, 4, 0, 0, None) == _native.MB_ERR_INVALID
     assert "overlap" in _native.last_error()
+    assert library.mb_copy(1 << 20, 2 << 20, 64, 256, 4, 0, 4, None) == _native.MB_ERR_INVALID  # unknown flag
+    assert "flags" in _native.last_error()
     assert library.mb_read_sum(0, 1 << 20, 2 << 20, 100, 100, 256, None) == _native.MB_ERR_INVALID
     assert library.mb_read_sum(7, 1 << 20, 2 << 20, 100, 1024, 256, None) == _native.MB_ERR_INVALID
     assert library.mb_copy(None, None, 0, 256, 4, 0, 0, None) == _native.MB_OK  # empty copy is a no-op

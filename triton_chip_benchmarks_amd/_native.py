@@ -22,6 +22,7 @@ MB_ERR_HIP = -3
 MB_ERR_ALIGNMENT = -4
 
 MB_COPY_NONTEMPORAL = 1
+MB_COPY_WRITE_THROUGH = 2
 
 MB_DTYPE_F32 = 0
 MB_DTYPE_F16 = 1

@@ -31,7 +31,7 @@ _PEAK_RE = re.compile(r"tensor_peak_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\
 _GEMM_RE = re.compile(r"gemm_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
 _GEMM_DMA_RE = re.compile(r"gemm_dma_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)E")
 _ELEM_BITS = {"bf16": 16, "f16": 16, "i8": 8, "fp8": 8, "mxfp4": 4, "f32": 32, "f64": 64}
-_COPY_RE = re.compile(r"copy_kernelI(Dv4_j|j|h)Li(\d+)ELb([01])E")
+_COPY_RE = re.compile(r"copy_kernelI(Dv4_j|j|h)Li(\d+)ELi([012])E")
 _READ_RE = re.compile(r"read_sum_kernelI(f|DF16_|t)Li(\d+)E")
 _VECTOR_RE = re.compile(r"vector_(\w+?)_kernelILi(\d+)E")
 _COPY_UNIT = {"Dv4_j": "dwordx4", "j": "dword", "h": "byte"}
@@ -55,8 +55,8 @@ def registered_name(symbol: str) -> str | None:
         return f"gemm_{fmt}_256x256x{int(row_bytes) * 8 // _ELEM_BITS[fmt]}"
     match = _COPY_RE.search(symbol)
     if match:
-        unit, vpt, nt = match.groups()
-        return f"copy_{_COPY_UNIT[unit]}_vpt{vpt}{'_nt' if nt == '1' else ''}"
+        unit, vpt, policy = match.groups()
+        return f"copy_{_COPY_UNIT[unit]}_vpt{vpt}{('', '_nt', '_stream')[int(policy)]}"
     match = _READ_RE.search(symbol)
     if match:
         dtype, vec = match.groups()

@@ -47,13 +47,29 @@ def copy_geometry(block_size, element_size, num_warps):
     return threads, per_thread if per_thread in (1, 2, 4, 8, 16) else None
 
 
+# Copy cache policies: plain, non-temporal loads and stores, or streaming
+# (non-temporal loads, device-scope stores written through the XCD's L2).
+COPY_POLICIES = {"off": 0, "on": _native.MB_COPY_NONTEMPORAL,
+                 "stream": _native.MB_COPY_NONTEMPORAL | _native.MB_COPY_WRITE_THROUGH}
+POLICY_SUFFIX = {"off": "", "on": "_nt", "stream": "_stream"}
+
+
+def copy_policy(nontemporal) -> str:
+    """Policy name from a bool (False/True) or a policy name."""
+    if isinstance(nontemporal, str):
+        if nontemporal not in COPY_POLICIES:
+            raise ValueError(f"unknown copy policy {nontemporal!r}")
+        return nontemporal
+    return "on" if nontemporal else "off"
+
+
 def launch_copy(src, dst, block_threads, vectors_per_thread, grid_blocks=0, nontemporal=False):
-    """dst <- src on the current stream through mb_copy."""
+    """dst <- src on the current stream through mb_copy; `nontemporal` is a bool or "off"/"on"/"stream"."""
     nbytes = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() != nbytes:
         raise ValueError("copy source and destination sizes differ")
     _native.call("mb_copy", src.data_ptr(), dst.data_ptr(), nbytes, block_threads, vectors_per_thread,
-                 grid_blocks, _native.MB_COPY_NONTEMPORAL if nontemporal else 0, _native.stream_handle())
+                 grid_blocks, COPY_POLICIES[copy_policy(nontemporal)], _native.stream_handle())
 
 
 def launch_read(src, sink, block_size, block_threads):
@@ -123,8 +139,9 @@ def parse_args(argv=None):
                         help="Elements per workgroup step (copy) or per block sum (read)")
     parser.add_argument("--num-warps", type=positive_int, nargs="+",
                         help="64-lane waves per workgroup (default: 1 4 8)")
-    parser.add_argument("--nontemporal", choices=("off", "on", "both"), default="both",
-                        help="Copy with streaming (nt) loads/stores (default: measure both)")
+    parser.add_argument("--nontemporal", choices=("off", "on", "stream", "both", "all"), default="all",
+                        help="Copy cache policy: off (plain), on (nt loads and stores), stream (nt loads, "
+                             "write-through device-scope stores), both (off+on) or all (default)")
     parser.add_argument("--grid-blocks", type=int, default=0,
                         help="Copy workgroups striding over the buffer; 0 = one per step (default)")
     parser.add_argument("--seed", type=int, default=0, help="Source RNG seed (uniform [-1, 1))")
@@ -144,7 +161,8 @@ def parse_args(argv=None):
 
 def configurations(args, element_size):
     warps = args.num_warps or ([4] if args.quick else [1, 4, 8])
-    nontemporal = {"off": [False], "on": [True], "both": [False, True]}[args.nontemporal]
+    nontemporal = {"off": ["off"], "on": ["on"], "stream": ["stream"], "both": ["off", "on"],
+                   "all": ["off", "on", "stream"]}[args.nontemporal]
     configs = []
     for block in args.block_sizes:
         for num_warps in warps:
@@ -185,7 +203,7 @@ def main(argv=None):
     print("Validation: masked tails passed; every measured output is checked in full.")
     print("Copy traffic = 2 * buffer bytes; read traffic = buffer bytes + FP32 reduction sink. "
           "GB/s and TB/s use decimal units; peak uses the shortest timed sample.")
-    print("mode   buffer MiB   block  warps  nt      min ms   median ms   peak GB/s  median GB/s  % of 8 TB/s")
+    print("mode   buffer MiB   block  warps  cache      min ms   median ms   peak GB/s  median GB/s  % of 8 TB/s")
     rows = []
     for size_mib in args.sizes_mib:
         buffer_bytes = size_mib * 2**20
@@ -224,7 +242,7 @@ def main(argv=None):
                                                  f"warps={warps}, nt={nontemporal}")
                         correctness = {"correctness": "passed (full output and masked tail)"}
                         write_bytes = buffer_bytes
-                        kernel = f"copy_dwordx4_vpt{per_thread}{'_nt' if nontemporal else ''}"
+                        kernel = f"copy_dwordx4_vpt{per_thread}{POLICY_SUFFIX[copy_policy(nontemporal)]}"
                     else:
                         sink = torch.full((-(-n // block),), float("nan"), device=device)
 
@@ -248,12 +266,14 @@ def main(argv=None):
                            "peak_gbps": peak_gbps, "peak_tbps": peak_gbps / 1000,
                            "fraction_of_hbm_peak": peak_gbps / roofline.HBM_PEAK_GBPS, **correctness}
                     if mode == "copy":
-                        row.update(vectors_per_thread=config["vectors_per_thread"], nontemporal=nontemporal,
+                        row.update(vectors_per_thread=config["vectors_per_thread"],
+                                   nontemporal=copy_policy(nontemporal) != "off",
+                                   cache_policy=copy_policy(nontemporal),
                                    grid_blocks=args.grid_blocks, seed=args.seed,
                                    source_distribution="uniform[-1, 1)")
                     rows.append(row)
-                    nt_label = "-" if nontemporal is None else ("on" if nontemporal else "off")
-                    print(f"{mode:4s} {size_mib:11d} {block:7d} {warps:6d} {nt_label:>3} "
+                    nt_label = "-" if nontemporal is None else copy_policy(nontemporal)
+                    print(f"{mode:4s} {size_mib:11d} {block:7d} {warps:6d} {nt_label:>6} "
                           f"{timings['min_ms']:11.6f} {timings['median_ms']:11.6f} {peak_gbps:11.2f} "
                           f"{gbps:12.2f} {100 * peak_gbps / roofline.HBM_PEAK_GBPS:11.1f}", flush=True)
                     del sink

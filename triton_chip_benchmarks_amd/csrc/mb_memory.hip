@@ -3,8 +3,11 @@
 // Copy: every lane moves 16-byte vectors (global_load_dwordx4 /
 // global_store_dwordx4); consecutive lanes touch consecutive vectors, so each
 // wave64 instruction covers 1 KiB of contiguous memory. A workgroup step holds
-// `vectors_per_thread` independent loads in flight before the stores, which is
-// what keeps enough bytes outstanding per CU to saturate HBM3E.
+// `vectors_per_thread` independent loads in flight before the stores. The
+// cache policy is a template argument: plain, non-temporal (nt loads and
+// stores), or streaming (nt loads, device-scope stores that write through the
+// XCD's L2 instead of leaving dirty lines to be evicted later) - on MI355X the
+// last measures ~1% faster than nt stores for HBM-sized copies.
 //
 // Read: one wave reduces one segment of `block_elements` values to a single
 // float (the reference's per-program sum), streaming it with 16-byte loads and
@@ -18,15 +21,31 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T, bool NT>
+// Copy cache policies.
+constexpr int kPlain = 0, kNontemporal = 1, kStream = 2;
+
+template <typename T, int POLICY>
 __device__ __forceinline__ T load_elem(const T* ptr) {
-  if constexpr (NT) return __builtin_nontemporal_load(ptr);
+  if constexpr (POLICY != kPlain) return __builtin_nontemporal_load(ptr);
   return *ptr;
 }
 
-template <typename T, bool NT>
+// Device-scope (sc1) vector stores; the compiler has no builtin for the scope bits.
+__device__ __forceinline__ void store_sc1(u32x4* ptr, u32x4 value) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(ptr), "v"(value) : "memory");
+}
+__device__ __forceinline__ void store_sc1(uint32_t* ptr, uint32_t value) {
+  asm volatile("global_store_dword %0, %1, off sc1" ::"v"(ptr), "v"(value) : "memory");
+}
+__device__ __forceinline__ void store_sc1(uint8_t* ptr, uint8_t value) {
+  asm volatile("global_store_byte %0, %1, off sc1" ::"v"(ptr), "v"(static_cast<uint32_t>(value)) : "memory");
+}
+
+template <typename T, int POLICY>
 __device__ __forceinline__ void store_elem(T* ptr, T value) {
-  if constexpr (NT) {
+  if constexpr (POLICY == kStream) {
+    store_sc1(ptr, value);
+  } else if constexpr (POLICY == kNontemporal) {
     __builtin_nontemporal_store(value, ptr);
   } else {
     *ptr = value;
@@ -34,7 +53,7 @@ __device__ __forceinline__ void store_elem(T* ptr, T value) {
 }
 
 // T is the access unit (u32x4, uint32_t or uint8_t); n counts units.
-template <typename T, int VPT, bool NT>
+template <typename T, int VPT, int POLICY>
 __global__ void __launch_bounds__(1024) copy_kernel(const T* __restrict__ src, T* __restrict__ dst,
                                                      uint64_t n) {
   const uint32_t block_threads = blockDim.x;
@@ -52,16 +71,16 @@ __global__ void __launch_bounds__(1024) copy_kernel(const T* __restrict__ src, T
     T values[VPT];
     if (left > static_cast<uint64_t>(VPT - 1) * threads) {
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) values[j] = load_elem<T, NT>(s + j * threads);
+      for (int j = 0; j < VPT; ++j) values[j] = load_elem<T, POLICY>(s + j * threads);
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) store_elem<T, NT>(d + j * threads, values[j]);
+      for (int j = 0; j < VPT; ++j) store_elem<T, POLICY>(d + j * threads, values[j]);
     } else {
 #pragma unroll
       for (int j = 0; j < VPT; ++j)
-        if (j * threads < left) values[j] = load_elem<T, NT>(s + j * threads);
+        if (j * threads < left) values[j] = load_elem<T, POLICY>(s + j * threads);
 #pragma unroll
       for (int j = 0; j < VPT; ++j)
-        if (j * threads < left) store_elem<T, NT>(d + j * threads, values[j]);
+        if (j * threads < left) store_elem<T, POLICY>(d + j * threads, values[j]);
     }
   }
 }
@@ -133,7 +152,7 @@ __global__ void __launch_bounds__(1024) read_sum_kernel(const T* __restrict__ sr
   }
 }
 
-template <typename T, bool NT>
+template <typename T, int POLICY>
 int launch_copy_units(const void* src, void* dst, uint64_t units, uint32_t threads, uint32_t vpt,
                       uint32_t grid_blocks, hipStream_t stream) {
   const uint64_t step = static_cast<uint64_t>(threads) * vpt;
@@ -147,27 +166,26 @@ int launch_copy_units(const void* src, void* dst, uint64_t units, uint32_t threa
   T* d = static_cast<T*>(dst);
   dim3 g(static_cast<uint32_t>(grid)), b(threads);
   switch (vpt) {
-    case 1: copy_kernel<T, 1, NT><<<g, b, 0, stream>>>(s, d, units); break;
-    case 2: copy_kernel<T, 2, NT><<<g, b, 0, stream>>>(s, d, units); break;
-    case 4: copy_kernel<T, 4, NT><<<g, b, 0, stream>>>(s, d, units); break;
-    case 8: copy_kernel<T, 8, NT><<<g, b, 0, stream>>>(s, d, units); break;
-    case 16: copy_kernel<T, 16, NT><<<g, b, 0, stream>>>(s, d, units); break;
+    case 1: copy_kernel<T, 1, POLICY><<<g, b, 0, stream>>>(s, d, units); break;
+    case 2: copy_kernel<T, 2, POLICY><<<g, b, 0, stream>>>(s, d, units); break;
+    case 4: copy_kernel<T, 4, POLICY><<<g, b, 0, stream>>>(s, d, units); break;
+    case 8: copy_kernel<T, 8, POLICY><<<g, b, 0, stream>>>(s, d, units); break;
+    case 16: copy_kernel<T, 16, POLICY><<<g, b, 0, stream>>>(s, d, units); break;
     default: return fail(MB_ERR_INVALID, "mb_copy: vectors_per_thread %u not in {1,2,4,8,16}", vpt);
   }
   return launch_status("copy_kernel");
 }
 
+#define MB_REGISTER_COPY_POLICY(T, TNAME, P, SUFFIX)                                          \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt1" SUFFIX, (copy_kernel<T, 1, P>));                  \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt2" SUFFIX, (copy_kernel<T, 2, P>));                  \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt4" SUFFIX, (copy_kernel<T, 4, P>));                  \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt8" SUFFIX, (copy_kernel<T, 8, P>));                  \
+  MB_REGISTER_KERNEL("copy_" TNAME "_vpt16" SUFFIX, (copy_kernel<T, 16, P>))
 #define MB_REGISTER_COPY(T, TNAME)                                                            \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt1", (copy_kernel<T, 1, false>));                     \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt2", (copy_kernel<T, 2, false>));                     \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt4", (copy_kernel<T, 4, false>));                     \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt8", (copy_kernel<T, 8, false>));                     \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt16", (copy_kernel<T, 16, false>));                   \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt1_nt", (copy_kernel<T, 1, true>));                   \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt2_nt", (copy_kernel<T, 2, true>));                   \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt4_nt", (copy_kernel<T, 4, true>));                   \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt8_nt", (copy_kernel<T, 8, true>));                   \
-  MB_REGISTER_KERNEL("copy_" TNAME "_vpt16_nt", (copy_kernel<T, 16, true>))
+  MB_REGISTER_COPY_POLICY(T, TNAME, kPlain, "");                                              \
+  MB_REGISTER_COPY_POLICY(T, TNAME, kNontemporal, "_nt");                                     \
+  MB_REGISTER_COPY_POLICY(T, TNAME, kStream, "_stream")
 
 MB_REGISTER_COPY(u32x4, "dwordx4");
 MB_REGISTER_COPY(uint32_t, "dword");
@@ -214,19 +232,29 @@ int mb_copy(const void* src, void* dst, uint64_t bytes, uint32_t block_threads, 
     return fail(MB_ERR_INVALID, "mb_copy: block_threads %u must be a multiple of 64 up to 1024", block_threads);
   if (!power_of_two(vectors_per_thread) || vectors_per_thread > 16)
     return fail(MB_ERR_INVALID, "mb_copy: vectors_per_thread %u not in {1,2,4,8,16}", vectors_per_thread);
-  if (flags & ~MB_COPY_NONTEMPORAL) return fail(MB_ERR_INVALID, "mb_copy: unknown flags 0x%x", flags);
+  if (flags & ~(MB_COPY_NONTEMPORAL | MB_COPY_WRITE_THROUGH))
+    return fail(MB_ERR_INVALID, "mb_copy: unknown flags 0x%x", flags);
   const char* s = static_cast<const char*>(src);
   char* d = static_cast<char*>(dst);
   if (s < d + bytes && d < s + bytes) return fail(MB_ERR_INVALID, "mb_copy: source and destination overlap");
-  const bool nt = flags & MB_COPY_NONTEMPORAL;
+  // Write-through stores pair with streaming loads; without it, the nt flag
+  // makes both loads and stores non-temporal.
+  const int policy = (flags & MB_COPY_WRITE_THROUGH) ? kStream : (flags & MB_COPY_NONTEMPORAL) ? kNontemporal : kPlain;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  auto units = [&](auto unit, const void* from, void* to, uint64_t count) {
+    using T = decltype(unit);
+    switch (policy) {
+      case kStream: return launch_copy_units<T, kStream>(from, to, count, block_threads, vectors_per_thread,
+                                                         grid_blocks, st);
+      case kNontemporal: return launch_copy_units<T, kNontemporal>(from, to, count, block_threads,
+                                                                   vectors_per_thread, grid_blocks, st);
+      default: return launch_copy_units<T, kPlain>(from, to, count, block_threads, vectors_per_thread,
+                                                   grid_blocks, st);
+    }
+  };
   if (aligned(src, 16) && aligned(dst, 16)) {
     const uint64_t vectors = bytes / 16;
-    int rc = nt ? launch_copy_units<u32x4, true>(src, dst, vectors, block_threads, vectors_per_thread,
-                                                 grid_blocks, st)
-                : launch_copy_units<u32x4, false>(src, dst, vectors, block_threads, vectors_per_thread,
-                                                  grid_blocks, st);
-    if (rc) return rc;
+    if (int rc = units(u32x4{}, src, dst, vectors)) return rc;
     const uint32_t tail = static_cast<uint32_t>(bytes % 16);
     if (tail) {
       copy_tail_kernel<<<1, 64, 0, st>>>(reinterpret_cast<const uint8_t*>(s + vectors * 16),
@@ -235,14 +263,8 @@ int mb_copy(const void* src, void* dst, uint64_t bytes, uint32_t block_threads, 
     }
     return MB_OK;
   }
-  if (aligned(src, 4) && aligned(dst, 4) && bytes % 4 == 0)
-    return nt ? launch_copy_units<uint32_t, true>(src, dst, bytes / 4, block_threads, vectors_per_thread,
-                                                  grid_blocks, st)
-              : launch_copy_units<uint32_t, false>(src, dst, bytes / 4, block_threads, vectors_per_thread,
-                                                   grid_blocks, st);
-  return nt ? launch_copy_units<uint8_t, true>(src, dst, bytes, block_threads, vectors_per_thread, grid_blocks, st)
-            : launch_copy_units<uint8_t, false>(src, dst, bytes, block_threads, vectors_per_thread, grid_blocks,
-                                                st);
+  if (aligned(src, 4) && aligned(dst, 4) && bytes % 4 == 0) return units(uint32_t{}, src, dst, bytes / 4);
+  return units(uint8_t{}, src, dst, bytes);
 }
 
 int mb_read_sum(int dtype, const void* src, float* sink, uint64_t elements, uint32_t block_elements,
