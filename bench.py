@@ -207,6 +207,21 @@ class PeakWorkload:
             f"{m}x{n}x{k} tiles, best repeat within {CPU_ROW_BUDGET_S:g} s")
 
 
+def host_description(torch) -> dict:
+    """The host the CPU baseline ran on: model name, logical CPUs, usable CPUs, torch threads."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "usable_cpus": usable,
+            "torch_threads": torch.get_num_threads(), "blas_threads": _blas_threads()}
+
+
 def _blas_threads():
     try:
         from threadpoolctl import threadpool_info
@@ -294,7 +309,7 @@ def main(argv=None):
                "unit": "% of MI355X peak (mean over headline rows)",
                "cores": max(r["cores"] for r in cpu_rows), "kind": "port",
                "sample": "; ".join(f"{r['row']}: {r['sample']}" for r in cpu_rows),
-               "host_cpu_count": os.cpu_count(), "rows": cpu_rows}
+               "host_cpu_count": os.cpu_count(), "host": host_description(torch), "rows": cpu_rows}
     line = {
         "metric": METRIC, "value": value, "unit": "% of MI355X peak (mean over headline rows)",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": total_ms / args.steps,

@@ -323,3 +323,47 @@ def test_bench_refuses_more_than_one_gpu():
                                capture_output=True, text=True, timeout=120)
     assert completed.returncode == 2
     assert "one MI355X" in completed.stdout + completed.stderr
+
+
+def test_resume_keeps_finished_rows_and_reruns_the_rest(tmp_path):
+    args = _args(tmp_path)
+
+    def first(item, args, directory):
+        status = "ok" if item.key in ("memory_capacity", "tensor_fp8") else \
+            "unsupported" if item.key == "tensor_tf32" else "error"
+        row = empty_metric(item, status, None if status == "ok" else "stand-in")
+        if status == "ok":
+            row["value"] = 1.0
+        return row, None
+
+    with mock.patch.object(suite, "run_metric", side_effect=first), contextlib.redirect_stdout(io.StringIO()):
+        suite.run_suite(args)
+    rerun = []
+
+    def second(item, args, directory):
+        rerun.append(item.key)
+        return empty_metric(item, "not_implemented", "second pass"), None
+
+    resumed_args = _args(tmp_path, "--resume")
+    with mock.patch.object(suite, "run_metric", side_effect=second), contextlib.redirect_stdout(io.StringIO()):
+        report = suite.run_suite(resumed_args)
+    kept = {"memory_capacity", "tensor_fp8", "tensor_tf32"}
+    assert set(rerun) == {m.key for m in METRICS} - kept
+    by_key = {row["metric"]: row for row in report["results"]}
+    assert by_key["tensor_fp8"]["resumed"] is True and by_key["tensor_fp8"]["value"] == 1.0
+    assert by_key["tensor_tf32"]["status"] == "unsupported"
+    assert by_key["vector_fp32"]["status"] == "not_implemented"
+
+
+def test_resume_ignores_a_report_of_another_mode_or_shape(tmp_path):
+    path = tmp_path / "report.json"
+    path.write_text(json.dumps({"schema_version": 1, "smoke_only": False,
+                                "results": [{"metric": m.key, "status": "ok"} for m in METRICS]}))
+    assert suite.resumable_rows(path, quick=True) == {}          # full report, smoke run
+    assert len(suite.resumable_rows(path, quick=False)) == 17
+    path.write_text(json.dumps({"schema_version": 1, "smoke_only": False,
+                                "results": [{"metric": "memory_capacity", "status": "ok"}]}))
+    assert suite.resumable_rows(path, quick=False) == {}         # not the 17-row table
+    path.write_text("not json")
+    assert suite.resumable_rows(path, quick=False) == {}
+    assert suite.resumable_rows(tmp_path / "missing.json", quick=False) == {}

@@ -53,6 +53,9 @@ def build_parser():
                         help="Maximum seconds per metric (default: 900)")
     parser.add_argument("--only", nargs="+", metavar="METRIC",
                         help="Run only these metric keys; the others stay 'skipped'")
+    parser.add_argument("--resume", action="store_true",
+                        help="Keep rows of an existing --output report that finished (ok, unverified, "
+                             "unsupported, not_implemented) and run only the others")
     parser.add_argument("--probe-device", action="store_true", help=argparse.SUPPRESS)
     return parser
 
@@ -136,11 +139,36 @@ def run_metric(metric, args, directory):
     return result, document
 
 
+FINISHED = ("ok", "unverified", "unsupported", "not_implemented")
+
+
+def resumable_rows(path, quick):
+    """Finished rows of an earlier report at `path`, by metric key.
+
+    Only a report of this schema, with the same 17 metric keys and the same
+    --quick setting, is reused; anything else resumes nothing.
+    """
+    try:
+        previous = json.loads(Path(path).read_text())
+    except (OSError, ValueError):
+        return {}
+    if not isinstance(previous, dict) or previous.get("schema_version") != 1:
+        return {}
+    rows = previous.get("results")
+    if not isinstance(rows, list) or [r.get("metric") for r in rows if isinstance(r, dict)] != \
+            [metric.key for metric in METRICS]:
+        return {}
+    if bool(previous.get("smoke_only")) != bool(quick):
+        return {}
+    return {row["metric"]: row for row in rows if row.get("status") in FINISHED}
+
+
 def run_suite(args):
     args.output = args.output.resolve()
     directory = (args.results_dir or args.output.with_name(args.output.stem + "_runs")).resolve()
     directory.mkdir(parents=True, exist_ok=True)
     selected = set(args.only) if getattr(args, "only", None) else None
+    resumed = resumable_rows(args.output, args.quick) if getattr(args, "resume", False) else {}
     if selected:
         unknown = selected - {metric.key for metric in METRICS}
         if unknown:
@@ -156,6 +184,12 @@ def run_suite(args):
     for index, metric in enumerate(METRICS):
         if selected is not None and metric.key not in selected:
             report["results"][index] = empty_metric(metric, "skipped", "not selected with --only")
+            continue
+        if metric.key in resumed:
+            report["results"][index] = dict(resumed[metric.key], resumed=True)
+            write_json(args.output, report)
+            print(f"[{index + 1}/{len(METRICS)}] {metric.key}: kept from the earlier report "
+                  f"({resumed[metric.key]['status']})", flush=True)
             continue
         print(f"[{index + 1}/{len(METRICS)}] {metric.key} ...", flush=True)
         result, document = run_metric(metric, args, directory)

@@ -1,0 +1,173 @@
+#!/usr/bin/env python3
+"""Independent cross-implementation check on one MI355X: two paths, same silicon limit.
+
+The tensor and memory rows come from this suite's own gfx950 kernels. Here the
+same work runs a second way on the same card, with each output checked
+against the other:
+  copy   mb_copy (the suite's kernel)  vs  dst.copy_(src) (hipMemcpy device-to-device)
+  GEMM   mb_gemm (the suite's kernel)  vs  torch.matmul / torch._scaled_mm / torch._int_mm (hipBLASLt)
+This follows the reference's practice of comparing its Triton suite with an
+independent Ascend C implementation on the same chip (ascendc/RESULTS.md:57-108):
+a large gap points at a kernel, not at the silicon. Rates use the suite's
+device-event timing (common.measure). The library paths are measurement
+references only; nothing in the suite's rows is taken from them.
+"""
+
+from __future__ import annotations
+
+import argparse
+from pathlib import Path
+import sys
+
+if __package__ in (None, ""):
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    from triton_chip_benchmarks_amd import _native, bench_bandwidth, gemm, roofline
+    from triton_chip_benchmarks_amd.common import add_common_arguments, emit_results, measure, setup_device
+else:
+    from . import _native, bench_bandwidth, gemm, roofline
+    from .common import add_common_arguments, emit_results, measure, setup_device
+
+COPY_SHAPE = {"block_threads": 64, "vectors_per_thread": 1, "policy": "stream"}
+GEMM_SIZE = 8192
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def copy_rows(args, sizes_mib):
+    """mb_copy against hipMemcpy device-to-device on the same buffers."""
+    torch = _torch()
+    rows = []
+    for size_mib in sizes_mib:
+        n = size_mib * 2**20 // 4
+        generator = torch.Generator(device="cuda").manual_seed(args.seed)
+        src = torch.empty(n, device="cuda", dtype=torch.float32).uniform_(-1, 1, generator=generator)
+        dst = torch.empty_like(src)
+        paths = {
+            "mb_copy": lambda: bench_bandwidth.launch_copy(src, dst, COPY_SHAPE["block_threads"],
+                                                           COPY_SHAPE["vectors_per_thread"], 0,
+                                                           COPY_SHAPE["policy"]),
+            "hipMemcpyDtoD": lambda: dst.copy_(src),
+        }
+        for name, run in paths.items():
+            dst.fill_(float("nan"))
+            run()
+            torch.cuda.synchronize()
+            if not torch.equal(src.view(torch.int32), dst.view(torch.int32)):
+                raise AssertionError(f"{name}: copy of {size_mib} MiB differs from its source")
+            timing = measure(run, args)
+            traffic = 2 * n * 4
+            peak = traffic / (timing["min_ms"] * 1e6)
+            rows.append({"check": "copy", "path": name, "buffer_mib": size_mib, "traffic_bytes": traffic,
+                         "peak_gbps": peak, "gbps": traffic / (timing["median_ms"] * 1e6),
+                         "fraction_of_hbm_peak": peak / roofline.HBM_PEAK_GBPS,
+                         "validation": "bit-exact against the source", **timing})
+    return rows
+
+
+def _library_gemm(dtype, a, b, torch):
+    """The library path for C = A . B^T (B stored [N][K]), or None when torch has none."""
+    if dtype in ("bf16", "fp16"):
+        bt = b.t()
+        return lambda: torch.matmul(a, bt)
+    if dtype == "fp8" and hasattr(torch, "_scaled_mm"):
+        one = torch.ones((), device=a.device, dtype=torch.float32)
+        bt = b.t()
+        return lambda: torch._scaled_mm(a, bt, scale_a=one, scale_b=one, out_dtype=torch.float32)
+    if dtype == "int8" and hasattr(torch, "_int_mm"):
+        bt = b.t()
+        return lambda: torch._int_mm(a, bt)
+    return None
+
+
+def gemm_rows(args, dtypes, size):
+    """mb_gemm against the torch (hipBLASLt) GEMM on the same operands; outputs cross-checked."""
+    torch = _torch()
+    rows = []
+    for dtype in dtypes:
+        a, b, c, scales, a_values, b_values = gemm.gemm_inputs(dtype, size, size, size, "cuda", args.seed)
+        del a_values, b_values
+        config = max(_native.gemm_configs(dtype), key=lambda cfg: cfg["tile_m"] * cfg["tile_n"])
+        ours = lambda: _native.gemm(dtype, config, a, b, c, size, size, size, *(scales or (None, None)))
+        ours()
+        torch.cuda.synchronize()
+        peak_value = roofline.PEAKS[f"tensor_{dtype}"][0]
+        library = None
+        try:
+            library = _library_gemm(dtype, a, b, torch)
+            if library is not None:
+                theirs = library()
+                torch.cuda.synchronize()
+        except RuntimeError as exc:  # the op exists but this build has no kernel for the dtype
+            library, reason = None, f"torch library path unavailable: {exc}".splitlines()[0]
+        else:
+            reason = None if library is not None else "torch has no library GEMM for this format"
+        agreement = None
+        if library is not None:
+            ref, got = theirs.double(), c.double()
+            scale = ref.abs().max().item() or 1.0
+            agreement = (got - ref).abs().max().item() / scale
+            tolerance = gemm.TOLERANCE[dtype] or 0.0
+            if agreement > max(tolerance, 1e-6 if dtype in ("fp8", "int8") else tolerance):
+                raise AssertionError(f"{dtype}: mb_gemm and the library disagree (normwise {agreement:.3g})")
+            del theirs, ref, got
+        for name, run in (("mb_gemm", ours), ("torch/hipBLASLt", library)):
+            if run is None:
+                rows.append({"check": "gemm", "path": name, "dtype": dtype, "m": size, "n": size, "k": size,
+                             "status": "unavailable", "reason": reason})
+                continue
+            timing = measure(run, args)
+            peak = 2 * size**3 / (timing["min_ms"] * 1e9)
+            rows.append({"check": "gemm", "path": name, "dtype": dtype, "m": size, "n": size, "k": size,
+                         "kernel": _native.gemm_kernel_name(dtype, config) if name == "mb_gemm" else "library",
+                         "peak_teraops_per_second": peak,
+                         "median_teraops_per_second": 2 * size**3 / (timing["median_ms"] * 1e9),
+                         "fraction_of_peak": peak / peak_value, "normwise_difference": agreement, **timing})
+        del a, b, c, scales
+        torch.cuda.empty_cache()
+    return rows
+
+
+def build_parser():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--copy-mib", type=int, nargs="+", default=[1024, 2048], help="copy buffer sizes (MiB)")
+    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8"],
+                        choices=["bf16", "fp16", "fp8", "int8"])
+    parser.add_argument("--gemm-size", type=int, default=GEMM_SIZE, help="square GEMM size (default 8192)")
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--quick", action="store_true", help="small sizes: a smoke check, not a measurement")
+    add_common_arguments(parser)
+    return parser
+
+
+def main(argv=None) -> int:
+    args = build_parser().parse_args(argv)
+    if args.quick:
+        args.copy_mib, args.gemm_size, args.warmup, args.rep, args.rounds = [8], 512, 5, 10, 3
+    metadata = setup_device(args)
+    rows = copy_rows(args, args.copy_mib) + gemm_rows(args, args.gemm_dtypes, args.gemm_size)
+    print(f"{'check':6s} {'path':18s} {'case':14s} {'peak':>12s} {'median':>12s} {'% peak':>7s}  note")
+    for row in rows:
+        if row.get("status") == "unavailable":
+            print(f"{row['check']:6s} {row['path']:18s} {row['dtype']:14s} {'-':>12s} {'-':>12s} {'-':>7s}  "
+                  f"{row['reason']}")
+            continue
+        if row["check"] == "copy":
+            case, peak, median, frac = f"{row['buffer_mib']} MiB", row["peak_gbps"], row["gbps"], \
+                row["fraction_of_hbm_peak"]
+            note = "GB/s"
+        else:
+            case, peak, median, frac = f"{row['dtype']} {row['m']}^3", row["peak_teraops_per_second"], \
+                row["median_teraops_per_second"], row["fraction_of_peak"]
+            note = "TFLOP/s" + (f", normwise diff {row['normwise_difference']:.2g}"
+                                if row.get("normwise_difference") is not None else "")
+        print(f"{row['check']:6s} {row['path']:18s} {case:14s} {peak:12.1f} {median:12.1f} {100 * frac:7.1f}  {note}")
+    emit_results("crosscheck", metadata, args, rows)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
