@@ -19,10 +19,12 @@ kernel's output is validated before timing with the product's own checks
 reference's tolerance for the MFMA rows).
 
 Timing: for each kernel in turn, W untimed warmup launches, then its K timed
-launches back to back between two torch.cuda.synchronize() calls, as the
-reference's batch timing does (common.py:295-534). MI355X raises its clock
-over ~40 ms when a matrix-bound kernel follows a memory-bound one, and the
-per-kernel warmup keeps that ramp out of the timed launches. A kernel's
+launches back to back - captured once into a HIP graph and replayed - between
+two torch.cuda.synchronize() calls, as the reference's batch timing does
+(common.py:295-534). The output of the timed launches is checked again.
+MI355X raises its clock over ~40 ms when a matrix-bound kernel follows a
+memory-bound one, and the per-kernel warmup keeps that ramp out of the timed
+launches. A kernel's
 ms_per_launch is its batch time between two HIP events on the launch stream
 over K (no event between launches, as in the reference's event batches);
 ms_per_step is the sum of the kernels' batch times over K.
@@ -123,13 +125,19 @@ class CopyWorkload:
         self.launcher(self.src, self.dst, COPY_CONFIG["block_threads"], COPY_CONFIG["vectors_per_thread"],
                       COPY_CONFIG["grid_blocks"], COPY_CONFIG["nontemporal"])
 
-    def validate(self):
+    def poison(self):
         self.dst.fill_(float("nan"))
-        self.launch()
+
+    def check(self):
         self.torch.cuda.synchronize()
         if not self.torch.equal(self.src.view(self.torch.int32), self.dst.view(self.torch.int32)):
             raise AssertionError("copy output differs from its source")
         return "bit-exact: every word of the 1 GiB destination equals the source"
+
+    def validate(self):
+        self.poison()
+        self.launch()
+        return self.check()
 
     def rate(self, ms):
         return self.work / (ms * 1e6)  # GB/s
@@ -176,14 +184,20 @@ class PeakWorkload:
     def launch(self):
         self.bt.launch_peak(self.dtype, self.config, self.a, self.b, self.c, PEAK_ITERATIONS, self.scales)
 
-    def validate(self):
+    def poison(self):
         self.c.fill_(float("nan"))
-        self.launch()
+
+    def check(self):
         reference = self.bt.exact_reference(self.values[0], self.values[1], PEAK_ITERATIONS, self.torch.float32)
         self.torch.cuda.synchronize()
         result = self.bt.validate_peak(self.c, reference, self.dtype, self.config["tile_k"], PEAK_ITERATIONS)
         return (f"every output within atol {result['atol']:.3g} of the exact float64 lattice reference "
                 f"(max error {result['max_abs_error']:.3g})")
+
+    def validate(self):
+        self.poison()
+        self.launch()
+        return self.check()
 
     def rate(self, ms):
         return self.work / (ms * 1e9)  # TFLOP/s
@@ -262,20 +276,43 @@ def main(argv=None):
     checks = {w.name: w.validate() for w in workloads}
 
     stream = torch.cuda.current_stream()
-    batch_ms = []
+    batch_ms, timing_modes = [], []
     for w in workloads:
         # W untimed warmup launches right before the kernel's K timed ones, so
         # the clock has settled at this kernel's load when timing starts.
         for _ in range(args.warmup):
             w.launch()
+        torch.cuda.synchronize()
+        # The K launches are captured once into a HIP graph and replayed, as the
+        # reference's event batches are (common.py:311-361); without graph
+        # support they are launched directly.
+        submit, mode = None, "hip_graph"
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(args.steps):
+                    w.launch()
+            graph.replay()  # untimed: the first replay uploads the graph
+            torch.cuda.synchronize()
+            submit = graph.replay
+        except RuntimeError:
+            torch.cuda.synchronize()
+            mode = "direct_launches"
+
+            def submit(w=w):
+                for _ in range(args.steps):
+                    w.launch()
+        w.poison()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record(stream)
-        for _ in range(args.steps):
-            w.launch()
+        submit()
         end.record(stream)
         torch.cuda.synchronize()
         batch_ms.append(start.elapsed_time(end))
+        timing_modes.append(mode)
+        w.check()  # raises if the timed launches' output is wrong
+        checks[w.name] += "; the same check passed again on the timed launches' output"
     total_ms = sum(batch_ms)
 
     traffic = traffic_table()
@@ -318,7 +355,10 @@ def main(argv=None):
         "data": "synthetic: seeded uniform fp32 copy source; exact-lattice MFMA operands, resident in HBM",
         "config": {"workload": " + ".join(w.name for w in workloads), "device": info["name"], "arch": info["arch"],
                    "compute_units": info["compute_units"], "peak_iterations": PEAK_ITERATIONS,
-                   "copy_elements": COPY_ELEMENTS, "timing": "K back-to-back launches per kernel, HIP events"},
+                   "copy_elements": COPY_ELEMENTS,
+                   "timing": "per kernel: W warmup launches, then K launches replayed from one HIP graph "
+                             "between two HIP events" if all(m == "hip_graph" for m in timing_modes)
+                             else "per kernel: W warmup launches, then K direct launches between two HIP events"},
         "roofline": roofline_block, "cpu_baseline": cpu, "rows": rows,
     }
     print(json.dumps(line))
