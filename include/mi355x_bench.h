@@ -195,6 +195,16 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
 #define MB_VECTOR_BF16_FMA 5  /* x <- bf16(fma(f32(x), a, b_c)), v_fma_f32 + v_cvt_pk_bf16_f32 */
 #define MB_VECTOR_FP8 6       /* always MB_ERR_UNSUPPORTED: no FP8 vector arithmetic on gfx950 */
 #define MB_VECTOR_FP4 7       /* always MB_ERR_UNSUPPORTED: no FP4 vector arithmetic on gfx950 */
+/* Widened (converted) FP8/FP4 chains, not native arithmetic: the state stays
+ * FP8 E4M3 / FP4 E2M1 (one code per byte in memory, a = Coefficients[0] and
+ * b_c = Coefficients[1+c] as codes too) and every update is
+ *   x <- narrow(fma(f32(x), f32(a), f32(b_c)))
+ * with v_cvt_pk_f32_fp8 / v_cvt_scalef32_pk_f32_fp4 (scale 1) widening a pair
+ * of chains, two v_fma_f32, and v_cvt_pk_fp8_f32 / v_cvt_scalef32_pk_fp4_f32
+ * rounding the pair back (round to nearest even). They replace the
+ * reference's Ascend C converted vector rows (ascendc/src/bench_vector.asc:335-572). */
+#define MB_VECTOR_FP8_WIDENED 8
+#define MB_VECTOR_FP4_WIDENED 9
 
 /* Registered kernel name of (kind, unroll), or NULL. */
 const char* mb_vector_kernel_name(int kind, uint32_t unroll);

@@ -204,3 +204,92 @@ def baseline_inputs(dtype: str, elements: int, rng: np.random.Generator):
     if dtype in ("fp16", "bf16"):
         return round_narrow(inputs, dtype), round_narrow(coefficients, dtype)
     return inputs, coefficients
+
+
+# ---- widened (converted) FP8 / FP4 chains -------------------------------------
+# The reference's Ascend C suite measures these rows as "converted" chains
+# (ascendc/src/bench_vector.asc:335-572): the state stays in the narrow format
+# and each update is x <- narrow(fma(f32(x), a, b_c)), one FP32 rounding then
+# one rounding to the narrow format, both to nearest even. The Ascend C check
+# uses the exact involution a = -1 (bench_vector.asc:1007-1012); the emulation
+# below also covers contractive coefficients, where every step rounds.
+
+FP8_E4M3_MAX = 448.0
+E2M1_MAX = 6.0
+_E2M1_MAGNITUDES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def round_fp8_e4m3fn(values) -> np.ndarray:
+    """Nearest E4M3FN value (ties to even): 3 fraction bits, exponents -6..8,
+    subnormal quantum 2^-9. Inputs must lie within +-448 (no saturation rule
+    is assumed beyond it)."""
+    y = np.asarray(values, dtype=np.float64)
+    if np.any(np.abs(y) > FP8_E4M3_MAX) or np.any(np.isnan(y)):
+        raise ValueError("E4M3FN rounding is only defined here for finite |x| <= 448")
+    magnitude = np.abs(y)
+    with np.errstate(divide="ignore"):
+        exponent = np.floor(np.log2(np.where(magnitude > 0, magnitude, 1.0)))
+    quantum = np.ldexp(1.0, (np.maximum(exponent, -6) - 3).astype(np.int64))
+    return np.copysign(np.rint(magnitude / quantum) * quantum, y)  # -0 and underflow keep the sign
+
+
+def encode_fp8_e4m3fn(values) -> np.ndarray:
+    """Codes of E4M3FN-representable values (vectorised; -0 keeps its sign bit)."""
+    y = np.asarray(values, dtype=np.float64)
+    sign = np.signbit(y).astype(np.int64) << 7
+    magnitude = np.abs(y)
+    with np.errstate(divide="ignore"):
+        exponent = np.floor(np.log2(np.where(magnitude > 0, magnitude, 1.0))).astype(np.int64)
+    normal = (magnitude >= 2.0**-6)
+    mantissa_normal = np.rint((magnitude / np.ldexp(1.0, exponent) - 1.0) * 8).astype(np.int64)
+    code_normal = ((exponent + 7) << 3) | mantissa_normal
+    code_sub = np.rint(magnitude / 2.0**-9).astype(np.int64)
+    codes = np.where(normal, code_normal, code_sub) | sign
+    if not np.array_equal(decode_fp8(codes), y):
+        raise ValueError("value not representable in E4M3FN")
+    return codes.astype(np.uint8)
+
+
+def decode_fp8(codes) -> np.ndarray:
+    from .tensor import fp8_e4m3fn_decode
+
+    return fp8_e4m3fn_decode(codes)
+
+
+def round_e2m1(values) -> np.ndarray:
+    """Nearest E2M1 value (ties to even): quantum 0.5 below 2, 1 in [2, 4), 2 in [4, 6]."""
+    y = np.asarray(values, dtype=np.float64)
+    if np.any(np.abs(y) > E2M1_MAX) or np.any(np.isnan(y)):
+        raise ValueError("E2M1 rounding is only defined here for finite |x| <= 6")
+    magnitude = np.abs(y)
+    quantum = np.where(magnitude < 2, 0.5, np.where(magnitude < 4, 1.0, 2.0))
+    return np.copysign(np.rint(magnitude / quantum) * quantum, y)
+
+
+def encode_e2m1(values) -> np.ndarray:
+    """Codes of E2M1-representable values (sign bit 3; -0 keeps its sign bit)."""
+    y = np.asarray(values, dtype=np.float64)
+    index = np.searchsorted(_E2M1_MAGNITUDES, np.abs(y))
+    if np.any(index >= 8) or not np.array_equal(_E2M1_MAGNITUDES[np.minimum(index, 7)], np.abs(y)):
+        raise ValueError("value not representable in E2M1")
+    return (index | (np.signbit(y).astype(np.int64) << 3)).astype(np.uint8)
+
+
+def run_widened_chains(fmt: str, codes, coefficient_codes, iterations: int) -> np.ndarray:
+    """Codes after `iterations` updates x <- narrow(f32(x * a + b_c)) of every chain.
+
+    codes [8, n] (one code per element), coefficient_codes [9] (a, b_0..b_7).
+    x * a + b_c is exact in float64 for these narrow operands, so casting it to
+    float32 is the single rounding of v_fma_f32; the narrow rounding follows.
+    """
+    from .tensor import e2m1_decode
+
+    decode = decode_fp8 if fmt == "fp8" else e2m1_decode
+    narrow = round_fp8_e4m3fn if fmt == "fp8" else round_e2m1
+    encode = encode_fp8_e4m3fn if fmt == "fp8" else encode_e2m1
+    x = decode(np.asarray(codes))
+    coefficients = decode(np.asarray(coefficient_codes))
+    a, b = coefficients[0], coefficients[1:, None]
+    for _ in range(iterations):
+        x = narrow(np.asarray(x * a + b, dtype=np.float32).astype(np.float64))
+    return encode(x)

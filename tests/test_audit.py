@@ -81,6 +81,16 @@ def test_fp64_without_mfma_is_simt_and_no_instruction_is_an_error():
         audit.audit_tensor(["v_add_f32 v0, v1, v2"], "bf16")
 
 
+def test_widened_rule_needs_fma_and_both_conversions():
+    fp8 = ["v_cvt_pk_f32_fp8_e32 v[0:1], v2", "v_fma_f32 v0, v0, s4, s5", "v_cvt_pk_fp8_f32 v2, v0, v1"]
+    assert audit.audit_widened(fp8, "fp8")["native_arithmetic_verified"] is False
+    for missing in range(3):
+        with pytest.raises(audit.VectorAuditError):
+            audit.audit_widened(fp8[:missing] + fp8[missing + 1:], "fp8")
+    with pytest.raises(audit.VectorAuditError):
+        audit.audit_widened(fp8, "fp4")
+
+
 def test_vector_rules():
     assert audit.audit_vector(["v_dot4_i32_i8 v0, v0, v1, v2"], "int8", "dp4a")["native_arithmetic_verified"]
     assert audit.audit_vector(["v_dot2_f32_bf16 v0, v1, v2, v3"], "bf16", "dot2")["native_arithmetic_verified"]
@@ -148,6 +158,13 @@ def test_every_vector_kernel_issues_its_native_instruction_and_no_mfma(listing):
         if kind == "bf16fma":
             result = audit.audit_vector(lines, "bf16", "fma")
             assert result["native_arithmetic_verified"] is False
+            continue
+        if kind in ("fp8w", "fp4w"):
+            result = audit.audit_widened(lines, kind[:3])
+            assert result["native_arithmetic_verified"] is False
+            unroll = int(name.rsplit("_u", 1)[1])
+            # 8 chains: one FP32 FMA and one narrowing per update in the unrolled body.
+            assert result["amdgcn_fp32_fma_instruction_sites"] >= 8 * unroll, (name, result)
             continue
         dtype, instruction = VECTOR_INSTRUCTION[kind]
         result = audit.audit_vector(lines, dtype, "native")

@@ -200,6 +200,11 @@ def test_child_commands_use_this_interpreter_and_explicit_precisions(tmp_path):
     assert Path(vector[2]).name == "bench_vector.py"
     for command in (tf32, capacity, bandwidth, vector):
         assert (ROOT / Path(command[2]).name).exists()
+    # --widened reaches only the FP8/FP4 vector children; by default no child gets it.
+    assert all("--widened" not in suite.metric_command(m, args, Path("x.json")) for m in suite.METRICS)
+    args.widened = True
+    widened = [m.key for m in suite.METRICS if "--widened" in suite.metric_command(m, args, Path("x.json"))]
+    assert widened == ["vector_fp8", "vector_fp4"]
 
 
 def test_failed_child_never_reuses_an_old_success(tmp_path):
@@ -367,3 +372,14 @@ def test_resume_ignores_a_report_of_another_mode_or_shape(tmp_path):
     path.write_text("not json")
     assert suite.resumable_rows(path, quick=False) == {}
     assert suite.resumable_rows(tmp_path / "missing.json", quick=False) == {}
+
+
+def test_widened_measurement_is_a_detail_never_the_row_value():
+    document = {"status": "not_implemented", "reason": "no FP8 VALU arithmetic",
+                "details": {"widened": {"peak_tflops": 30.0, "tflops": 29.0,
+                                        "arithmetic_kind": "converted_fp32_fma_fp8_e4m3_state"}}}
+    row = summarize(metric("vector_fp8"), document)
+    assert row["status"] == "not_implemented" and row["value"] is None
+    assert row["widened_measurement"]["peak_tflops"] == 30.0
+    table = format_table([row])
+    assert "widened" in table and "not native" in table

@@ -134,3 +134,84 @@ def test_product_validators_accept_kernel_output_and_agree_with_oracle(gpu):
         if dtype in ("fp16", "bf16"):
             bench_vector.check_narrow_steps(inputs, output, coefficients, 4096, dtype, lanes=512)
 
+
+
+# ---- widened (converted) FP8 / FP4 chains -------------------------------------
+
+def _run_widened(kind, codes, coefficient_codes, iterations, unroll, block=256):
+    import torch
+
+    from triton_chip_benchmarks_amd import bench_vector
+
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    assert codes.shape[0] == 8 and codes.shape[1] % block == 0 and len(coefficient_codes) == 9
+    x = torch.from_numpy(codes).cuda()
+    c = torch.from_numpy(np.ascontiguousarray(coefficient_codes, dtype=np.uint8)).cuda()
+    out = torch.full_like(x, 0x7F)
+    bench_vector.launch_vector(kind, x, out, c, iterations, unroll, block)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+@pytest.mark.parametrize("iterations,unroll", [(7, 1), (8, 4), (32, 16)])
+def test_widened_involution_matches_oracle(gpu, fmt, iterations, unroll):
+    from triton_chip_benchmarks_amd import bench_vector
+
+    codes, coefficients = bench_vector.widened_inputs(fmt, 1024, "cpu", seed=iterations)
+    codes, coefficients = codes.numpy(), coefficients.numpy()
+    got = _run_widened(f"{fmt}_widened", codes, coefficients, iterations, unroll)
+    expected = ov.run_widened_chains(fmt, codes, coefficients, iterations)
+    assert np.array_equal(got, expected)
+    assert np.array_equal(got, codes if iterations % 2 == 0 else expected)
+
+
+def _finite_fp8_codes(rng, shape, max_magnitude):
+    values = ot.fp8_e4m3fn_decode(np.arange(256))
+    allowed = np.flatnonzero(~np.isnan(values) & (np.abs(values) <= max_magnitude))
+    return rng.choice(allowed, shape).astype(np.uint8)
+
+
+@pytest.mark.parametrize("iterations,unroll", [(1, 1), (3, 1), (24, 8)])
+@pytest.mark.parametrize("a", [0.875, -0.5, 0.9375, -0.0625])
+def test_widened_fp8_rounds_every_step_like_the_oracle(gpu, a, iterations, unroll):
+    """Contractive chains over every finite E4M3 code (subnormals, signed zeros,
+    up to 448): |x a + b| stays within 448, so each of the 24 steps rounds twice
+    (FP32, then E4M3) and the codes must agree bit for bit; short chains keep
+    the start codes' variety, long ones reach the fixed points."""
+    rng = np.random.default_rng(int(abs(a) * 1e4))
+    codes = _finite_fp8_codes(rng, (8, 2048), 448.0)
+    coefficients = np.concatenate([ov.encode_fp8_e4m3fn(np.array([a])), _finite_fp8_codes(rng, 8, 8.0)])
+    got = _run_widened("fp8_widened", codes, coefficients, iterations, unroll)
+    assert np.array_equal(got, ov.run_widened_chains("fp8", codes, coefficients, iterations))
+
+
+@pytest.mark.parametrize("iterations,unroll", [(1, 1), (16, 4)])
+@pytest.mark.parametrize("a", [0.5, -0.5, -1.0])
+def test_widened_fp4_rounds_every_step_like_the_oracle(gpu, a, iterations, unroll):
+    """Every E2M1 code as a start value; |b| <= 3 keeps |x a + b| <= 6 (for
+    a = -1, |x| <= 3 as well), so no step leaves the format's range."""
+    rng = np.random.default_rng(int(abs(a) * 10))
+    limit = 3.0 if a == -1.0 else 6.0
+    values = ot.e2m1_decode(np.arange(16))
+    codes = rng.choice(np.flatnonzero(np.abs(values) <= limit), (8, 1024)).astype(np.uint8)
+    b_codes = rng.choice(np.flatnonzero(np.abs(values) <= 3.0), 8).astype(np.uint8)
+    coefficients = np.concatenate([ov.encode_e2m1(np.array([a])), b_codes])
+    got = _run_widened("fp4_widened", codes, coefficients, iterations, unroll)
+    assert np.array_equal(got, ov.run_widened_chains("fp4", codes, coefficients, iterations))
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+def test_widened_flag_keeps_the_row_status_and_reports_details(gpu, tmp_path, fmt):
+    import json
+
+    from triton_chip_benchmarks_amd import bench_vector
+
+    output = tmp_path / f"vector_{fmt}.json"
+    bench_vector.main(["--dtype", fmt, "--widened", "--quick", "--output", str(output)])
+    document = json.loads(output.read_text())
+    assert document["status"] == ("not_implemented" if fmt == "fp8" else "unsupported")
+    widened = document["details"]["widened"]
+    assert widened["peak_tflops"] > 0 and widened["arithmetic_kind"].startswith("converted_fp32_fma")
+    row = document["details"]["widened_rows"][0]
+    assert row["native_arithmetic_verified"] is False and row["max_abs_error"] == 0.0

@@ -263,3 +263,126 @@ def test_block_sums_exact_on_integer_lattice_and_tolerance_rejects_errors():
     assert memory.cache_regime(512 * 2**20, 256 * 2**20, False) == ("cache_sensitive", False)
     assert memory.cache_regime(2**30, 0, False) == ("unknown_l2", False)
     assert math.isclose(memory.read_tolerance(np.ones(1024), 1024)[0], 1024 * 2 * 2**-23 * 10 + 1e-6)
+
+
+# ---- widened FP8/FP4 chains ------------------------------------------------------
+
+def _nearest_by_table(y, table, codes):
+    """Brute-force round to nearest over a value table; ties go to the code with mantissa bit 0."""
+    best = None
+    for value, code in zip(table, codes):
+        if np.isnan(value):
+            continue
+        distance = abs(y - value)
+        if best is None or distance < best[0] or (distance == best[0] and (code & 1) == 0 and (best[2] & 1)):
+            best = (distance, value, code)
+    return best[1]
+
+
+def test_fp8_rounding_matches_torch_on_float32_inputs():
+    import torch
+
+    rng = np.random.default_rng(1)
+    y = (rng.uniform(-440, 440, 100000) * np.exp(rng.uniform(-14, 0, 100000))).astype(np.float32)
+    expected = torch.from_numpy(y).to(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    assert np.array_equal(ov.round_fp8_e4m3fn(y.astype(np.float64)), expected)
+
+
+def test_fp8_rounding_matches_brute_force_and_ties_go_to_even():
+    table, codes = ot.fp8_e4m3fn_decode(np.arange(128)), np.arange(128)
+    grid = np.concatenate([np.linspace(0, 2.0**-5, 301), np.linspace(0.9, 2.1, 241), np.linspace(200, 448, 249)])
+    for y in grid:
+        assert ov.round_fp8_e4m3fn(y) == _nearest_by_table(y, table, codes), y
+    # 1 + 1/16 lies halfway between 1 and 1.125: even mantissa (1.0) wins; 1 + 3/16 goes to 1.25.
+    assert ov.round_fp8_e4m3fn([1.0625, 1.1875]).tolist() == [1.0, 1.25]
+
+
+def test_e2m1_rounding_matches_brute_force_and_known_ties():
+    codes = np.arange(8)
+    table = ot.e2m1_decode(codes)
+    for y in np.linspace(0, 6, 97):
+        assert ov.round_e2m1(y) == _nearest_by_table(y, table, codes), y
+        assert ov.round_e2m1(-y) == -_nearest_by_table(y, table, codes)
+    assert ov.round_e2m1([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0]).tolist() == [0, 1, 1, 2, 2, 4, 4]
+
+
+def test_widened_codes_round_trip():
+    fp8_values = ot.fp8_e4m3fn_decode(np.arange(256))
+    finite = ~np.isnan(fp8_values)
+    assert np.array_equal(ot.fp8_e4m3fn_decode(ov.encode_fp8_e4m3fn(fp8_values[finite])), fp8_values[finite])
+    assert np.array_equal(ov.encode_e2m1(ot.e2m1_decode(np.arange(16))), np.arange(16))
+    with pytest.raises(ValueError):
+        ov.encode_e2m1([2.5])
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+def test_widened_involution_is_exact(fmt):
+    """a = -1: x -> b - x -> x, exactly, on the lattices the Ascend C suite uses."""
+    rng = np.random.default_rng(3)
+    if fmt == "fp8":
+        x = rng.integers(1, 8, (8, 64)) / 8.0
+        b = np.arange(1, 9) / 8.0
+        encode = ov.encode_fp8_e4m3fn
+    else:
+        x = rng.choice([-1.0, -0.5, 0.0, 0.5, 1.0], (8, 64))
+        b = np.array([-0.5, 0.0, 0.5, -0.5, 0.0, 0.5, -0.5, 0.0])
+        encode = ov.encode_e2m1
+    codes, coeff = encode(x), encode(np.concatenate([[-1.0], b]))
+    decode = ot.fp8_e4m3fn_decode if fmt == "fp8" else ot.e2m1_decode
+    assert np.array_equal(decode(ov.run_widened_chains(fmt, codes, coeff, 7)), b[:, None] - x)
+    assert np.array_equal(ov.run_widened_chains(fmt, codes, coeff, 8), codes)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+def test_widened_contractive_chain_matches_exact_stepwise_rounding(fmt):
+    from fractions import Fraction
+
+    rng = np.random.default_rng(4)
+    if fmt == "fp8":
+        x = rng.integers(-15, 16, (8, 16)) / 16.0
+        coefficients = np.concatenate([[0.875], rng.integers(-7, 8, 8) / 32.0])
+        table, codes_all = ot.fp8_e4m3fn_decode(np.arange(128)), np.arange(128)
+        encode = ov.encode_fp8_e4m3fn
+    else:
+        x = rng.choice([-1.5, -1.0, -0.5, 0.0, 0.5, 1.0, 1.5], (8, 16))
+        coefficients = np.concatenate([[0.5], rng.choice([-1.0, -0.5, 0.5, 1.0], 8)])
+        table, codes_all = ot.e2m1_decode(np.arange(8)), np.arange(8)
+        encode = ov.encode_e2m1
+    got = ov.run_widened_chains(fmt, encode(x), encode(coefficients), 5)
+    state = x.copy()
+    for _ in range(5):
+        for c in range(8):
+            for i in range(state.shape[1]):
+                exact = Fraction(float(state[c, i])) * Fraction(float(coefficients[0])) + \
+                    Fraction(float(coefficients[1 + c]))
+                f32 = float(np.float32(float(exact)))  # exact in float64, one rounding to float32
+                magnitude = _nearest_by_table(abs(f32), table, codes_all)
+                state[c, i] = -magnitude if f32 < 0 else magnitude
+    decode = ot.fp8_e4m3fn_decode if fmt == "fp8" else ot.e2m1_decode
+    assert np.array_equal(np.abs(decode(got)), np.abs(state))
+    assert np.array_equal(np.sign(decode(got)), np.sign(state))
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+def test_widened_chains_keep_ieee_signed_zeros(fmt):
+    """IEEE 754 (6.3): -0 + -0 is -0, an exact zero sum of opposite signs is +0
+    under round-to-nearest, and a negative value that rounds to zero keeps its
+    sign; the narrow codes carry the sign bit (E4M3 0x80, E2M1 0x8)."""
+    encode = ov.encode_fp8_e4m3fn if fmt == "fp8" else ov.encode_e2m1
+    negative_zero = 0x80 if fmt == "fp8" else 0x8
+    x = np.array([[0.0, -0.0, 1.0, -0.0]] * 8)
+    # a = -0.5: +0 * a = -0; -0 * a = +0; 1 * a = -0.5.
+    for b, expected in ((-0.0, [negative_zero, 0, None, 0]), (0.0, [0, 0, None, 0]), (0.5, [None, None, 0, None])):
+        coefficients = encode(np.array([-0.5] + [b] * 8))
+        got = ov.run_widened_chains(fmt, encode(x), coefficients, 1)[0]
+        for column, code in enumerate(expected):
+            if code is not None:
+                assert got[column] == code, (fmt, b, column, got)
+    if fmt == "fp8":
+        # -2^-11 is below half the subnormal quantum 2^-9 / 2: rounds to -0.
+        tiny = encode(np.array([[-2.0**-9] * 4] * 8))
+        got = ov.run_widened_chains(fmt, tiny, encode(np.array([0.125] + [0.0] * 8)), 1)
+        assert (got == negative_zero).all()
+    else:
+        got = ov.run_widened_chains(fmt, encode(np.array([[-0.5] * 4] * 8)), encode(np.array([0.5] + [0.0] * 8)), 1)
+        assert (got == negative_zero).all()  # -0.25 ties to the even -0

@@ -292,6 +292,36 @@ _VECTOR_RULES = {
 }
 
 
+_WIDENED_CONVERSIONS = {
+    "fp8": (r"v_cvt_pk_f32_fp8(?:_e32|_e64|_sdwa)?", r"v_cvt_pk_fp8_f32(?:_e64)?"),
+    "fp4": (r"v_cvt_scalef32_pk_f32_fp4", r"v_cvt_scalef32_pk_fp4_f32"),
+}
+
+
+def audit_widened(lines: list[str], dtype: str) -> dict:
+    """Converted FP8/FP4 chains: the kernel must widen, FMA in FP32 and narrow.
+
+    The rows are never native (gfx950's VALU has no FP8/FP4 arithmetic): the
+    check is that each update is the stated v_fma_f32 between a widening and
+    a narrowing conversion of the format, with no matrix instruction.
+    """
+    if any(line.startswith(m) for line in lines for m in MATRIX_MNEMONICS):
+        raise VectorAuditError("Generated AMDGCN contains matrix instructions in a vector benchmark")
+    names = [mnemonic(line) for line in lines]
+    fma = [n for n in names if re.fullmatch(r"v_fmac?_f32(?:_e(?:32|64))?", n)]
+    widen_pattern, narrow_pattern = _WIDENED_CONVERSIONS[dtype]
+    widen = [n for n in names if re.fullmatch(widen_pattern, n)]
+    narrow = [n for n in names if re.fullmatch(narrow_pattern, n)]
+    if not (fma and widen and narrow):
+        raise VectorAuditError(f"Widened {dtype.upper()} kernel lacks v_fma_f32 or a {dtype.upper()} conversion")
+    return {"amdgcn_contains_matrix_instructions": False, "native_arithmetic_verified": False,
+            "amdgcn_fp32_fma_instruction_sites": len(fma),
+            "amdgcn_widen_instruction_sites": len(widen), "amdgcn_narrow_instruction_sites": len(narrow),
+            "amdgcn_instruction_types": sorted(set(fma + widen + narrow)),
+            "assembly_check": (f"converted, not native: {dtype.upper()} state widened to FP32, one v_fma_f32 "
+                               "per update, narrowed back")}
+
+
 def audit_vector(lines: list[str], dtype: str, operation: str) -> dict:
     """gfx950 vector audit (bench_vector.py:679-770 rules, gfx950 mnemonics).
 

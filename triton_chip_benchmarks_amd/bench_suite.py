@@ -56,6 +56,9 @@ def build_parser():
     parser.add_argument("--resume", action="store_true",
                         help="Keep rows of an existing --output report that finished (ok, unverified, "
                              "unsupported, not_implemented) and run only the others")
+    parser.add_argument("--widened", action="store_true",
+                        help="Also measure converted FP8/FP4 vector chains; they stay details of the "
+                             "not_implemented/unsupported rows, never a row value")
     parser.add_argument("--probe-device", action="store_true", help=argparse.SUPPRESS)
     return parser
 
@@ -73,6 +76,8 @@ def metric_command(metric, args, output):
             extra += ["--input-precision", "tf32" if metric.precision == "tf32" else "ieee"]
     else:
         script, extra = "bench_vector.py", ["--dtype", metric.precision]
+        if getattr(args, "widened", False) and metric.precision in ("fp8", "fp4"):
+            extra.append("--widened")
     command = [sys.executable, "-u", str(ROOT / script), *extra,
                "--device", str(args.device), "--timing", args.timing,
                "--warmup", str(args.warmup), "--rep", str(args.rep),

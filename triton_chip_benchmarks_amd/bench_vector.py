@@ -21,19 +21,20 @@ import sys
 
 if __package__ in (None, ""):
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
-    from triton_chip_benchmarks_amd import _native, audit, roofline
+    from triton_chip_benchmarks_amd import _native, audit, formats, roofline
     from triton_chip_benchmarks_amd.common import (add_common_arguments, available_memory_bytes,
                                                    emit_not_implemented, emit_results, emit_unsupported,
                                                    get_device, measure, positive_int, setup_device)
 else:
-    from . import _native, audit, roofline
+    from . import _native, audit, formats, roofline
     from .common import (add_common_arguments, available_memory_bytes, emit_not_implemented, emit_results,
                          emit_unsupported, get_device, measure, positive_int, setup_device)
 
 CHAINS = 8
 DEFAULT_ITERATIONS = 4096
 DTYPES = ("bf16", "fp16", "fp32", "int8", "fp64", "fp8", "fp4")
-KINDS = {"fp32": 0, "fp16": 1, "bf16_dot2": 2, "fp64": 3, "int8": 4, "bf16_fma": 5, "fp8": 6, "fp4": 7}
+KINDS = {"fp32": 0, "fp16": 1, "bf16_dot2": 2, "fp64": 3, "int8": 4, "bf16_fma": 5, "fp8": 6, "fp4": 7,
+         "fp8_widened": 8, "fp4_widened": 9}
 # (kernel kind, source operation, result-name suffix) per dtype, best-first.
 VARIANTS = {"fp32": [("fp32", "FMA", "fma")], "fp64": [("fp64", "FMA", "fma")], "fp16": [("fp16", "FMA", "fma")],
             "bf16": [("bf16_dot2", "DOT2_BF16", "dot2"), ("bf16_fma", "WIDENED_FMA", "widened_fma")],
@@ -72,7 +73,8 @@ def _torch():
 def storage_dtype(kind: str):
     torch = _torch()
     return {"fp32": torch.float32, "fp64": torch.float64, "fp16": torch.float16, "bf16_dot2": torch.bfloat16,
-            "bf16_fma": torch.bfloat16, "int8": torch.int32}[kind]
+            "bf16_fma": torch.bfloat16, "int8": torch.int32, "fp8_widened": torch.uint8,
+            "fp4_widened": torch.uint8}[kind]
 
 
 def isa_probe() -> dict:
@@ -294,6 +296,9 @@ def build_parser():
     parser.add_argument("--inputs", choices=("reference", "baseline"), default="reference",
                         help="Operand set: the reference's (default) or BASELINE.json's a=0.999, c=1e-3 workload")
     parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--widened", action="store_true",
+                        help="FP8/FP4: also measure converted chains (narrow state, FP32 FMA per update); the "
+                             "row keeps its not_implemented/unsupported status and the rate goes to details")
     parser.add_argument("--quick", action="store_true", help="One smoke configuration; not a peak result")
     return parser
 
@@ -413,6 +418,103 @@ def run_benchmark(args, metadata):
     emit_results(name, {**metadata, "vector_excluded_configurations": excluded}, args, rows)
 
 
+# ---- widened (converted) FP8 / FP4 chains ----------------------------------------
+# Not native arithmetic: gfx950's VALU has FP8/FP4 conversions but no FP8/FP4
+# math. The state stays in the narrow format and each update is
+# x <- narrow(fma(f32(x), a, b_c)), the reference's Ascend C "converted" rows
+# (ascendc/src/bench_vector.asc:335-572): only the FMA's 2 operations count.
+WIDENED_KIND = {"fp8": "fp8_widened", "fp4": "fp4_widened"}
+WIDENED_ARITHMETIC = {"fp8": "converted_fp32_fma_fp8_e4m3_state", "fp4": "converted_fp32_fma_fp4_e2m1_state"}
+
+
+def widened_inputs(dtype: str, elements: int, device, seed: int = 0):
+    """Codes for the exact involution the Ascend C suite validates (a = -1): x0
+    and b_c on the format's lattice so that b_c - x0 is exact
+    (ascendc/src/bench_vector.asc:912-950)."""
+    torch = _torch()
+    generator = torch.Generator().manual_seed(seed)
+    if dtype == "fp8":
+        x = torch.randint(1, 8, (CHAINS, elements), generator=generator).double() / 8
+        b = torch.arange(1, CHAINS + 1).double() / 8
+        encode = lambda v: v.float().to(torch.float8_e4m3fn).view(torch.uint8)
+    else:
+        x = (torch.randint(0, 5, (CHAINS, elements), generator=generator).double() - 2) * 0.5
+        b = (torch.arange(CHAINS).double() % 3 - 1) * 0.5
+        encode = formats.e2m1_encode
+    coefficients = torch.cat([torch.tensor([-1.0], dtype=torch.float64), b])
+    return encode(x).to(device), encode(coefficients).to(device)
+
+
+def widened_values(dtype: str, codes):
+    torch = _torch()
+    return codes.view(torch.float8_e4m3fn).double() if dtype == "fp8" else formats.e2m1_decode(codes)
+
+
+def check_widened(dtype: str, inputs, output, coefficients, iterations: int) -> dict:
+    """a = -1 returns x0 after an even count and b_c - x0 after an odd one, exactly."""
+    torch = _torch()
+    x0 = widened_values(dtype, inputs)
+    b = widened_values(dtype, coefficients)[1:, None]
+    expected = x0 if iterations % 2 == 0 else b - x0
+    got = widened_values(dtype, output)
+    if not torch.equal(got, expected):
+        raise AssertionError(f"widened {dtype} chains differ from the exact involution")
+    return {"correctness": "exact involution (a = -1): every element equals x0 or b - x0", "max_abs_error": 0.0}
+
+
+def run_widened(args, metadata) -> dict:
+    """Sweep the converted kernel; returns the details block for the status document."""
+    torch = _torch()
+    device = get_device(args)
+    dtype, kind = args.dtype, WIDENED_KIND[args.dtype]
+    fp32_issue = roofline.ISSUED_CEILINGS["vector_fp32"][0]  # one v_fma_f32 per update
+    print(f"{dtype.upper()} widened vector chains (not native arithmetic): {CHAINS} chains, {args.iterations} "
+          "iterations, narrow state, FP32 FMA per update")
+    rows = []
+    for blocks_per_sm in args.blocks_per_sm:
+        for block in args.block_sizes:
+            if block % 64 or block > 1024:
+                continue
+            elements = blocks_per_sm * metadata["sm_count"] * block
+            inputs, coefficients = widened_inputs(dtype, elements, device, args.seed)
+            output = torch.empty_like(inputs)
+            for unroll in args.unroll:
+                if args.iterations % unroll:
+                    continue
+                kernel = _native.load().mb_vector_kernel_name(KINDS[kind], unroll).decode()
+                assembly = audit.audit_widened(audit.instructions(kernel), dtype)
+                output.fill_(255)
+
+                def run(iterations=args.iterations, unroll_value=unroll, inputs=inputs, output=output,
+                        coefficients=coefficients, block=block):
+                    launch_vector(kind, inputs, output, coefficients, iterations, unroll_value, block)
+
+                run()
+                torch.cuda.synchronize()
+                correctness = check_widened(dtype, inputs, output, coefficients, args.iterations)
+                timing = measure(run, args)
+                rates = throughput_fields(dtype, elements, args.iterations, timing)
+                rows.append({"status": "ok", "requested_dtype": dtype, "operation": "WIDENED_FMA",
+                             "arithmetic_kind": WIDENED_ARITHMETIC[dtype], "arithmetic_dtype": "fp32",
+                             "input_storage_dtype": "fp8_e4m3fn" if dtype == "fp8" else "fp4_e2m1",
+                             "native_arithmetic_verified": False, "conversions_per_update": 1,
+                             "blocks_per_sm": blocks_per_sm, "block_size": block, "unroll": unroll,
+                             "elements_per_chain": elements, "kernel": kernel, **rates, **timing,
+                             **correctness, **assembly,
+                             "fraction_of_fp32_fma_issue_ceiling": rates["peak_tflops"] / fp32_issue})
+                print(f"widened {blocks_per_sm:4d} {block:6d} {unroll:4d} {timing['median_ms']:10.5f} "
+                      f"{rates['tflops']:8.3f} {rates['peak_tflops']:8.3f}", flush=True)
+            del inputs, output, coefficients
+    if not rows:
+        raise RuntimeError("No widened configuration produced a valid measurement")
+    best = max(rows, key=lambda row: row["peak_tflops"])
+    print(f"Widened {dtype.upper()} chains: {best['peak_tflops']:.3f} TFLOP/s (not a native {dtype.upper()} rate)")
+    return {"widened": {key: best[key] for key in ("kernel", "peak_tflops", "tflops", "arithmetic_kind",
+                                                   "blocks_per_sm", "block_size", "unroll", "correctness")},
+            "widened_rows": [{k: v for k, v in row.items() if k not in ("samples_ms_per_launch", "batch_samples_ms")}
+                             for row in rows]}
+
+
 def main(argv=None):
     parser = build_parser()
     args = parser.parse_args(argv)
@@ -424,15 +526,16 @@ def main(argv=None):
     configure_sweep(args)
     if any(args.iterations % unroll for unroll in args.unroll):
         parser.error("--iterations must be divisible by every --unroll factor")
+    details = run_widened(args, metadata) if args.widened and args.dtype in WIDENED_KIND else None
     reason = unsupported_dtype_reason(args.dtype)
     if reason:
         metadata["vector_fp4_capability_probe"] = isa_probe()
-        emit_unsupported(f"vector_{args.dtype}", metadata, args, reason)
+        emit_unsupported(f"vector_{args.dtype}", metadata, args, reason, details=details)
         return
     reason = not_implemented_dtype_reason(args.dtype)
     if reason:
         metadata["vector_fp8_capability_probe"] = isa_probe()
-        emit_not_implemented(f"vector_{args.dtype}", metadata, args, reason)
+        emit_not_implemented(f"vector_{args.dtype}", metadata, args, reason, details=details)
         return
     try:
         run_benchmark(args, metadata)

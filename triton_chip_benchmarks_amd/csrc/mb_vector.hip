@@ -16,6 +16,12 @@
 //   i8   x <- dot4(bytes(x), W) + b_c            v_dot4_i32_i8: the int32 state's
 //        four signed bytes times the packed weights, plus an int32 bias
 //        (the reference's DP4A feedback form, bench_vector.py:134-145).
+//   fp8 / fp4 widened (not native arithmetic: gfx950 has no FP8/FP4 VALU math)
+//        x <- narrow(fma(f32(x), a, b_c)) with the state kept in FP8 E4M3 or
+//        FP4 E2M1, two chains per conversion: v_cvt_pk_f32_fp8 or
+//        v_cvt_scalef32_pk_f32_fp4 (scale 1), two v_fma_f32, then
+//        v_cvt_pk_fp8_f32 or v_cvt_scalef32_pk_fp4_f32 (the reference's Ascend C
+//        "converted" rows, ascendc/src/bench_vector.asc:335-572).
 // The dot instructions are written as inline assembly so the VOP3P form with a
 // separate addend is issued (the compiler otherwise picks the accumulating
 // VOP2 form and spends moves to set up its destination). One asm block holds a
@@ -234,6 +240,77 @@ __global__ void __launch_bounds__(1024) vector_dot4_kernel(const int32_t* __rest
   for (int c = 0; c < CHAINS; ++c) out[c * elements + i] = x[c];
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// FP8 E4M3 state, one code per byte in memory; chains (2p, 2p+1) share the low
+// 16 bits of one VGPR.
+template <int UNROLL>
+__global__ void __launch_bounds__(1024) vector_fp8w_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out,
+                                                           const uint8_t* __restrict__ coeff, uint64_t elements,
+                                                           uint32_t trips) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint32_t x[CHAINS / 2];
+  float b[CHAINS];
+  const float a = __builtin_amdgcn_cvt_pk_f32_fp8(coeff[0], false)[0];
+#pragma unroll
+  for (int p = 0; p < CHAINS / 2; ++p) {
+    x[p] = in[(2 * p) * elements + i] | (static_cast<uint32_t>(in[(2 * p + 1) * elements + i]) << 8);
+    const f32x2 bp = __builtin_amdgcn_cvt_pk_f32_fp8(coeff[1 + 2 * p] | (coeff[2 + 2 * p] << 8), false);
+    b[2 * p] = bp[0];
+    b[2 * p + 1] = bp[1];
+  }
+  for (uint32_t t = 0; t < trips; ++t) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int p = 0; p < CHAINS / 2; ++p) {
+        const f32x2 v = __builtin_amdgcn_cvt_pk_f32_fp8(x[p], false);
+        x[p] = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_fmaf(v[0], a, b[2 * p]),
+                                               __builtin_fmaf(v[1], a, b[2 * p + 1]), x[p], false);
+      }
+  }
+#pragma unroll
+  for (int p = 0; p < CHAINS / 2; ++p) {
+    out[(2 * p) * elements + i] = static_cast<uint8_t>(x[p]);
+    out[(2 * p + 1) * elements + i] = static_cast<uint8_t>(x[p] >> 8);
+  }
+}
+
+// FP4 E2M1 state, one code per byte (low nibble) in memory; chains (2p, 2p+1)
+// share one byte (low nibble = chain 2p) of one VGPR.
+template <int UNROLL>
+__global__ void __launch_bounds__(1024) vector_fp4w_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out,
+                                                           const uint8_t* __restrict__ coeff, uint64_t elements,
+                                                           uint32_t trips) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint32_t x[CHAINS / 2];
+  float b[CHAINS];
+  const float a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(coeff[0] & 15u, 1.0f, 0)[0];
+#pragma unroll
+  for (int p = 0; p < CHAINS / 2; ++p) {
+    x[p] = (in[(2 * p) * elements + i] & 15u) | ((in[(2 * p + 1) * elements + i] & 15u) << 4);
+    const f32x2 bp =
+        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((coeff[1 + 2 * p] & 15u) | ((coeff[2 + 2 * p] & 15u) << 4), 1.0f, 0);
+    b[2 * p] = bp[0];
+    b[2 * p + 1] = bp[1];
+  }
+  for (uint32_t t = 0; t < trips; ++t) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int p = 0; p < CHAINS / 2; ++p) {
+        const f32x2 v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(x[p], 1.0f, 0);
+        x[p] = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(x[p], __builtin_fmaf(v[0], a, b[2 * p]),
+                                                        __builtin_fmaf(v[1], a, b[2 * p + 1]), 1.0f, 0);
+      }
+  }
+#pragma unroll
+  for (int p = 0; p < CHAINS / 2; ++p) {
+    out[(2 * p) * elements + i] = static_cast<uint8_t>(x[p] & 15u);
+    out[(2 * p + 1) * elements + i] = static_cast<uint8_t>((x[p] >> 4) & 15u);
+  }
+}
+
 using VectorLauncher = void (*)(const void*, void*, const void*, uint64_t, uint32_t, uint32_t, uint32_t,
                                 hipStream_t);
 
@@ -251,6 +328,8 @@ MB_VECTOR_LAUNCHER(vector_f16_kernel, _Float16)
 MB_VECTOR_LAUNCHER(vector_bf16dot_kernel, uint16_t)
 MB_VECTOR_LAUNCHER(vector_bf16fma_kernel, uint16_t)
 MB_VECTOR_LAUNCHER(vector_dot4_kernel, int32_t)
+MB_VECTOR_LAUNCHER(vector_fp8w_kernel, uint8_t)
+MB_VECTOR_LAUNCHER(vector_fp4w_kernel, uint8_t)
 
 struct VectorVariant {
   int kind;
@@ -274,6 +353,8 @@ const VectorVariant kVectorVariants[] = {
     MB_VECTOR_UNROLLS(MB_VECTOR_BF16_DOT2, vector_bf16dot_kernel, uint16_t, "vector_bf16dot"),
     MB_VECTOR_UNROLLS(MB_VECTOR_BF16_FMA, vector_bf16fma_kernel, uint16_t, "vector_bf16fma"),
     MB_VECTOR_UNROLLS(MB_VECTOR_I8_DOT4, vector_dot4_kernel, int32_t, "vector_dot4"),
+    MB_VECTOR_UNROLLS(MB_VECTOR_FP8_WIDENED, vector_fp8w_kernel, uint8_t, "vector_fp8w"),
+    MB_VECTOR_UNROLLS(MB_VECTOR_FP4_WIDENED, vector_fp4w_kernel, uint8_t, "vector_fp4w"),
 };
 
 struct VectorRegistrar {

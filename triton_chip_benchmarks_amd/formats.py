@@ -42,3 +42,15 @@ def e8m0_decode(codes):
 
     values = torch.pow(2.0, codes.double() - E8M0_BIAS)
     return torch.where(codes == 255, torch.full_like(values, float("nan")), values)
+
+
+def e2m1_encode(values):
+    """E2M1 codes of values on the E2M1 lattice (raises for any other value)."""
+    import torch
+
+    magnitudes = torch.tensor(E2M1_MAGNITUDES, dtype=torch.float64, device=values.device)
+    v = values.double()
+    index = torch.bucketize(v.abs(), magnitudes)
+    if bool((index > 7).any()) or not torch.equal(magnitudes[index.clamp(max=7)], v.abs()):
+        raise ValueError("values are not all on the E2M1 lattice")
+    return (index | (torch.signbit(v).to(torch.int64) << 3)).to(torch.uint8)

@@ -117,6 +117,10 @@ def summarize(metric, document):
     status = document.get("status")
     if status in ("unsupported", "not_implemented", "error", "unavailable"):
         result.update(status=status, reason=document.get("reason", status))
+        widened = (document.get("details") or {}).get("widened") if isinstance(document.get("details"), dict) else None
+        if isinstance(widened, dict):
+            # A converted (widened) measurement is a detail of the row, never its value.
+            result["widened_measurement"] = widened
         return result
     if metric.key == "memory_capacity":
         capacity = document.get("device", {}).get("total_memory_bytes")
@@ -184,6 +188,10 @@ def format_table(results):
             notes.append(f"{item['metric']}: {item['reason']}")
         if item.get("smoke_only"):
             notes.append(f"{item['metric']}: smoke test; not a peak result")
+        widened = item.get("widened_measurement")
+        if isinstance(widened, dict) and widened.get("peak_tflops"):
+            notes.append(f"{item['metric']}: widened ({widened.get('arithmetic_kind', 'converted')}) "
+                         f"{widened['peak_tflops']:.3f} TFLOP/s - not native arithmetic, not the row value")
         if item.get("execution_kind") == "simt":
             notes.append(f"{item['metric']}: measured matrix rate using SIMT scalar/vector instructions "
                          "(no native tensor MMA)")
