@@ -383,3 +383,13 @@ def test_widened_measurement_is_a_detail_never_the_row_value():
     assert row["widened_measurement"]["peak_tflops"] == 30.0
     table = format_table([row])
     assert "widened" in table and "not native" in table
+
+
+@pytest.mark.parametrize("script", ["bench_tensor.py", "bench_vector.py", "bench_bandwidth.py", "bench_suite.py",
+                                    "crosscheck.py"])
+def test_package_scripts_import_when_run_directly(script):
+    """Each benchmark module also runs as a plain script (its own import branch)."""
+    completed = subprocess.run([sys.executable, str(ROOT / "triton_chip_benchmarks_amd" / script), "--help"],
+                               capture_output=True, text=True, timeout=120, check=False)
+    assert completed.returncode == 0, completed.stderr[-2000:]
+    assert "usage" in completed.stdout

@@ -522,7 +522,7 @@ def main(argv=None) -> None:
     if args.mode == "peak":
         run_peak(args, metadata, device)
         return
-    from . import gemm
+    from triton_chip_benchmarks_amd import gemm  # absolute: also valid when this file runs as a script
 
     gemm.run_gemm(args, metadata, device)
 
