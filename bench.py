@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark of the MI355X peak-throughput suite (one JSON line).
 
-Metric (BASELINE.json): "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of
+Metric: "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of
 MI355X peak". One step is one pass of the hot path over resident synthetic
 inputs - one launch of each headline kernel:
   hbm_copy    mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from seed 0) into a
@@ -55,8 +55,8 @@ COPY_SEED = 0
 # policy: nt loads, device-scope stores written through the L2 (~1% over nt stores).
 COPY_CONFIG = {"block_threads": 64, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": "stream"}
 PEAK_ITERATIONS = 1024
-# (tile M, N, K, chains, workgroups per CU). BF16 is BASELINE's resident
-# variant; FP8 and MXFP4 use the fastest tiles of the bench_tensor sweep.
+# (tile M, N, K, chains, workgroups per CU). BF16 is the headline resident
+# variant (256x256x64 tile); FP8 and MXFP4 use the fastest tiles of the bench_tensor sweep.
 PEAK_SHAPES = {"bf16": (256, 256, 64, 1, 2), "fp8": (128, 128, 128, 2, 4), "fp4": (128, 128, 256, 2, 4)}
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_per_launch.txt"
 CPU_ROW_BUDGET_S = 4.0  # host seconds per row: about 16 s of CPU work in all

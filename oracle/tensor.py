@@ -147,7 +147,7 @@ def fp64_precision_probe() -> tuple[np.ndarray, np.ndarray]:
 
 
 def gemm_reference(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """C = A @ B in float64 (bench_tensor.py:277-286); exact on the BASELINE lattices."""
+    """C = A @ B in float64 (bench_tensor.py:277-286); exact on the benchmark's operand lattices."""
     return np.matmul(np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64))
 
 

@@ -188,7 +188,7 @@ def reference_inputs(dtype: str, elements: int, rng: np.random.Generator):
 
 
 def baseline_inputs(dtype: str, elements: int, rng: np.random.Generator):
-    """BASELINE.json's vector workload: a0 ~ U[0.5, 1), b = 0.999, c = 1e-3.
+    """The headline vector workload: a0 ~ U[0.5, 1), b = 0.999, c = 1e-3.
 
     INT8: a0 in [-4, 4], weights 1 in every byte, bias 1 (wrapping int32). The
     float values are rounded to the storage format as the device sees them.

@@ -1,9 +1,9 @@
 """GPU parity of the MFMA GEMM kernels (mb_gemm) against oracle.tensor.
 
 Small and ragged shapes are compared element by element with the float64
-oracle; operands are exact lattices (or the BASELINE sets, which are exact in
+oracle; operands are exact lattices (or the benchmark's GEMM sets, which are exact in
 fp32 accumulation), so the comparison is exact, except FP64 with N(0,1)
-operands (normwise 1e-12). BASELINE's full sizes are checked through
+operands (normwise 1e-12). The benchmark's full sizes are checked through
 size-independent properties: exact row and column checksums
 (1^T C = (1^T A) B and C 1 = A (B 1)) plus exactly recomputed sampled rows.
 """
@@ -102,7 +102,7 @@ def test_gemm_matches_oracle_every_tile_and_ragged_shapes(gpu, dtype):
 @pytest.mark.parametrize("dtype,size", [("bf16", 8192), ("fp8", 8192), ("int8", 8192), ("fp4", 16384),
                                         ("fp64", 4096)])
 def test_gemm_baseline_size_checksums(gpu, dtype, size):
-    """BASELINE sizes: exact row/column checksums and sampled rows against the oracle."""
+    """Benchmark sizes: exact row/column checksums and sampled rows against the oracle."""
     config = max(_configs(dtype), key=lambda c: c["tile_m"] * c["tile_n"])
     print(f"gemm {dtype} {size}^3 tile {config['tile_m']}x{config['tile_n']}x{config['tile_k']}", flush=True)
     rng = np.random.default_rng(size)

@@ -3,7 +3,7 @@
 Copy is bit-exact; block sums stay within the reference's float32 summation
 bound (bench_bandwidth.py:81-110). Cases cover ragged sizes, every access
 width (16-byte, dword, byte), misaligned pointers, grid-stride launches and the
-BASELINE size of 2^28 fp32 through size-independent properties.
+headline size of 2^28 fp32 through size-independent properties.
 """
 
 import numpy as np

@@ -45,7 +45,7 @@ def _encode(torch, values, dtype):
 
 def _operands(rng, dtype, blocks, m, n, k, chains):
     if dtype == "fp8":
-        palette = np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0])  # BASELINE set: products exact in fp32
+        palette = np.array([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0])  # FP8 GEMM set: products exact in fp32
         return palette[rng.integers(0, 6, (blocks, m, k))], palette[rng.integers(0, 6, (chains, blocks, k, n))]
     if dtype == "int8":
         return (rng.integers(-8, 9, (blocks, m, k)).astype(np.float64),

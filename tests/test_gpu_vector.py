@@ -3,7 +3,7 @@
 The oracle emulates every update with exactly the kernels' rounding (one
 rounding for fp32/fp64/fp16 FMA; bf16 states rounded from the fp32 result),
 so outputs are compared bit for bit, on the reference's operands, on
-BASELINE.json's operands and on random operands that exercise rounding.
+the headline workload's operands and on random operands that exercise rounding.
 """
 
 import zlib

@@ -164,7 +164,7 @@ def fp4_peak_inputs(blocks: int, config: dict, device, seed: int = 0, palette=(1
     """Packed MX FP4 operands, unit scales and their exact values (bench_tensor.py:614-644).
 
     The default palette holds the codes of +-0.5 and +-1.0; any subset of the
-    16 codes may be passed (the BASELINE GEMM uses all 16).
+    16 codes may be passed (the MXFP4 GEMM configuration uses all 16).
     """
     torch = _torch()
     m, n, k, chains = config["tile_m"], config["tile_n"], config["tile_k"], config["chains"]
@@ -445,7 +445,7 @@ def build_parser():
     parser.add_argument("--blocks-per-sm", nargs="+", type=int, default=[1, 2, 4, 8],
                         help="launched workgroups per CU (default: 1 2 4 8)")
     parser.add_argument("--sizes", nargs="+", type=int, default=None,
-                        help="square GEMM dimensions M=N=K (default: the BASELINE size of the format)")
+                        help="square GEMM dimensions M=N=K (default: the headline size of the format)")
     parser.add_argument("--dtype", choices=DTYPES, default="fp16",
                         help="matrix input format; TF32 uses FP32 storage; FP8 is E4M3FN and FP4 is OCP MX E2M1")
     parser.add_argument("--input-precision", choices=("ieee", "tf32"),

@@ -129,7 +129,7 @@ def make_inputs(dtype: str, elements: int, device, inputs_kind: str = "reference
       x0 ~ U[0.125, 1), a = 1 - 2^-14, b_c = (c+1) 2^-16; fp16/bf16 the exact
       involution x0 in {1..7}/8, a = -1, b_c = (c+1)/8; int8 random int32 words,
       W = bytes (3, -2, 1, -1), b_c = c + 1.
-    baseline: BASELINE.json's vector workload - x0 ~ U[0.5, 1), a = 0.999,
+    baseline: the headline vector workload - x0 ~ U[0.5, 1), a = 0.999,
       b = 1e-3; int8 x0 in [-4, 4], W = bytes (1, 1, 1, 1), b = 1.
     """
     torch = _torch()
@@ -294,7 +294,7 @@ def build_parser():
     parser.add_argument("--unroll", type=int, choices=[1, 4, 8, 16], nargs="+",
                         help="Updates per loop trip (default: 1 4 8 16)")
     parser.add_argument("--inputs", choices=("reference", "baseline"), default="reference",
-                        help="Operand set: the reference's (default) or BASELINE.json's a=0.999, c=1e-3 workload")
+                        help="Operand set: the reference's (default) or the headline a=0.999, c=1e-3 workload")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--widened", action="store_true",
                         help="FP8/FP4: also measure converted chains (narrow state, FP32 FMA per update); the "

@@ -1,5 +1,5 @@
-// Dense GEMM on the matrix cores (tensor rows' GEMM mode and BASELINE's
-// 8192^3 / 4096^3 / 16384^3 configurations).
+// Dense GEMM on the matrix cores (tensor rows' GEMM mode and the benchmark's
+// 8192^3 / 4096^3 / 16384^3 GEMM configurations).
 //
 // C[M][N] = A[M][K] . B[K][N] with A row-major and B column-major, so both
 // operands are K-contiguous in memory ("NT"); the accumulator type is the

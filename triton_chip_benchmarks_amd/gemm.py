@@ -2,7 +2,7 @@
 
 Follows the reference's run_gemm (bench_tensor.py:1509-1595): per size and
 tile, validate C against a full-precision reference, then time the kernel and
-report 2*M*N*K operations. Operands follow BASELINE.json's GEMM configurations:
+report 2*M*N*K operations. Operands follow the benchmark's GEMM configurations:
   bf16/fp16/fp32/fp64  N(0, 1) from the seed; normwise relative tolerance
                        (1e-2 for bf16/fp16, 1e-5 for fp32, 1e-12 for fp64)
   fp8 (E4M3FN)         values from {+-0.5, +-1, +-2}; every product and partial
