@@ -1,0 +1,111 @@
+"""CPU tests of how bench_vector classifies each vector configuration.
+
+The reference's vector benchmark (bench_vector.py:623-799, 1054-1268;
+tests/test_vector_dtypes.py, tests/test_vector_compilation.py) keeps rates
+only from kernels whose assembly passes the audit and whose output passes the
+closed-form check: an audit rejection excludes the configuration (and makes
+the row "unsupported" when nothing is left), a spilling kernel is excluded,
+and a wrong result is an error. The native launch, the instruction listing
+and the timer are stand-ins here; the launch stand-in computes the chains with
+the oracle, so the real validation code judges real recurrences.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import vector as ov
+from triton_chip_benchmarks_amd import bench_vector as bv
+
+NATIVE_FP32 = ["v_fma_f32 v0, v1, s2, v0"]
+
+
+def _args(tmp_path, dtype):
+    parser = bv.build_parser()
+    args = parser.parse_args(["--dtype", dtype, "--iterations", "8", "--blocks-per-sm", "1", "--block-sizes", "64",
+                              "--unroll", "1", "--output", str(tmp_path / "vector.json")])
+    bv.configure_sweep(args)
+    return args
+
+
+class _Library:
+    @staticmethod
+    def mb_vector_kernel_name(kind, unroll):
+        return f"vector_stand_in_{kind}_u{unroll}".encode()
+
+
+@pytest.fixture
+def stand_ins(monkeypatch):
+    state = {"timed": 0, "corrupt": False, "listing": list(NATIVE_FP32), "spills": 0}
+
+    def launch(kind, inputs, output, coefficients, iterations, unroll, block):
+        assert kind == "fp32", kind
+        result = ov.run_chains("fp32", inputs.numpy(), coefficients.numpy(), iterations)
+        if state["corrupt"]:
+            result = np.array(result, copy=True)
+            result.flat[5] += 1e-3
+        output.copy_(torch.from_numpy(np.asarray(result)).to(output.dtype))
+
+    def measure(fn, args):
+        state["timed"] += 1
+        return {"median_ms": 2.0, "min_ms": 1.0, "timing_method": "stand-in"}
+
+    monkeypatch.setattr(bv, "get_device", lambda args: "cpu")
+    monkeypatch.setattr(bv, "available_memory_bytes", lambda: None)
+    monkeypatch.setattr(bv._native, "load", lambda: _Library())
+    monkeypatch.setattr(bv, "launch_vector", launch)
+    monkeypatch.setattr(bv, "measure", measure)
+    monkeypatch.setattr(bv.audit, "instructions", lambda kernel: list(state["listing"]))
+    monkeypatch.setattr(bv.audit, "resources",
+                        lambda kernel: {"registers_per_thread": 32, "register_spills": state["spills"]})
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *args, **kwargs: None)
+    return state
+
+
+def _run(tmp_path, dtype="fp32"):
+    args = _args(tmp_path, dtype)
+    bv.run_benchmark(args, {"sm_count": 2})
+    return json.loads((tmp_path / "vector.json").read_text())
+
+
+def test_audited_and_correct_kernel_is_timed_with_reference_op_counts(tmp_path, stand_ins):
+    document = _run(tmp_path)
+    assert document["status"] == "ok" and stand_ins["timed"] == 1
+    row = document["results"][0]
+    assert row["native_arithmetic_verified"] is True
+    # 2 flops per update x 8 chains x elements (1 WG/CU x 2 CUs x 64 lanes) x 8 iterations.
+    assert row["counted_flops"] == 2 * 8 * (2 * 64) * 8
+    assert row["peak_tflops"] == pytest.approx(row["counted_flops"] / 1e9)
+
+
+def test_kernel_without_native_instruction_is_unsupported_and_never_timed(tmp_path, stand_ins):
+    stand_ins["listing"] = ["v_mul_f32 v0, v1, v2", "v_add_f32 v0, v0, v3"]
+    with pytest.raises(bv.UnsupportedVectorDtype, match="v_fma|native"):
+        bv.run_benchmark(_args(tmp_path, "fp32"), {"sm_count": 2})
+    assert stand_ins["timed"] == 0
+
+
+def test_matrix_instruction_in_a_vector_kernel_is_excluded(tmp_path, stand_ins):
+    stand_ins["listing"] = NATIVE_FP32 + ["v_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]"]
+    with pytest.raises(bv.UnsupportedVectorDtype, match="matrix"):
+        bv.run_benchmark(_args(tmp_path, "fp32"), {"sm_count": 2})
+    assert stand_ins["timed"] == 0
+
+
+def test_spilling_kernel_is_excluded_and_nothing_is_reported(tmp_path, stand_ins):
+    stand_ins["spills"] = 4
+    with pytest.raises(RuntimeError, match="spills"):
+        bv.run_benchmark(_args(tmp_path, "fp32"), {"sm_count": 2})
+    assert stand_ins["timed"] == 0
+
+
+def test_wrong_result_is_an_error_before_timing(tmp_path, stand_ins):
+    stand_ins["corrupt"] = True
+    with pytest.raises(RuntimeError, match="correctness failed"):
+        _run(tmp_path)
+    assert stand_ins["timed"] == 0
+    assert not (tmp_path / "vector.json").exists()
