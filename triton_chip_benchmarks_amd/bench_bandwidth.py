@@ -19,12 +19,11 @@ if __package__ in (None, ""):
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
     from triton_chip_benchmarks_amd import _native, roofline
     from triton_chip_benchmarks_amd.common import (add_common_arguments, available_memory_bytes, emit_results,
-                                                   emit_unsupported, get_device, measure, positive_int,
-                                                   setup_device)
+                                                   get_device, measure, positive_int, setup_device)
 else:
     from . import _native, roofline
-    from .common import (add_common_arguments, available_memory_bytes, emit_results, emit_unsupported,
-                         get_device, measure, positive_int, setup_device)
+    from .common import (add_common_arguments, available_memory_bytes, emit_results, get_device, measure,
+                         positive_int, setup_device)
 
 DTYPE_CODES = {"fp32": _native.MB_DTYPE_F32, "fp16": _native.MB_DTYPE_F16, "bf16": _native.MB_DTYPE_BF16}
 VECTOR_BYTES = 16

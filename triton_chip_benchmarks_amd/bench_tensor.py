@@ -15,7 +15,6 @@ TF32 has no gfx950 instruction and is reported unsupported.
 from __future__ import annotations
 
 import argparse
-import math
 from pathlib import Path
 import sys
 

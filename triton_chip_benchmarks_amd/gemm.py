@@ -17,7 +17,7 @@ is a float64 torch.matmul on the device, exact on the integer-valued sets.
 from __future__ import annotations
 
 from . import _native, audit, formats, roofline
-from .common import available_memory_bytes, emit_results, emit_unsupported, measure
+from .common import available_memory_bytes, emit_unsupported, measure
 
 DEFAULT_SIZES = {"bf16": [8192], "fp16": [8192], "fp32": [8192], "fp8": [8192], "int8": [8192], "fp64": [4096],
                  "fp4": [16384]}
