@@ -1,0 +1,50 @@
+"""GPU test of the headline line's contract: one JSON line with every field the
+driver reads, a roofline block for the dominant kernel and a CPU baseline.
+
+The run is short (2 timed launches per kernel after 1 warmup) and exercises
+the same code path as the default run.
+"""
+
+import json
+import math
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+TOP_LEVEL = {"metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+             "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline", "rows"}
+
+
+def test_bench_prints_one_contract_line(gpu):
+    completed = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--steps", "2", "--warmup", "1"],
+                               cwd=ROOT, capture_output=True, text=True, timeout=600, check=False)
+    assert completed.returncode == 0, completed.stderr[-3000:]
+    lines = [line for line in completed.stdout.splitlines() if line.strip()]
+    assert len(lines) == 1, lines
+    line = json.loads(lines[0])
+    assert TOP_LEVEL <= set(line), TOP_LEVEL - set(line)
+    assert line["metric"] == "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of MI355X peak"
+    assert (line["n_gpus"], line["steps"], line["warmup"]) == (1, 2, 1)
+    assert line["higher_is_better"] is True and line["vs_baseline"] is None
+    assert "workload" in line["config"] and "model" not in line["config"]
+    rows = {row["name"]: row for row in line["rows"]}
+    assert set(rows) == {"hbm_copy", "peak_bf16", "peak_fp8", "peak_mxfp4"}
+    fractions = [row["frac"] for row in rows.values()]
+    assert all(0.3 < frac < 1.0 for frac in fractions), fractions
+    assert line["value"] == pytest.approx(100 * sum(fractions) / len(fractions))
+    assert line["ms_per_step"] == pytest.approx(sum(row["ms_per_launch"] for row in rows.values()))
+    roofline = line["roofline"]
+    assert {"bound", "achieved", "peak", "unit", "frac", "traffic"} <= set(roofline)
+    assert roofline["bound"] in ("hbm", "mfma")
+    assert roofline["frac"] == pytest.approx(roofline["achieved"] / roofline["peak"])
+    dominant = max(rows.values(), key=lambda row: row["ms_per_launch"])
+    assert roofline["kernel"] == dominant["kernel"]
+    baseline = line["cpu_baseline"]
+    assert {"value", "unit", "cores", "kind", "sample"} <= set(baseline)
+    assert baseline["kind"] in ("port", "reference") and baseline["cores"] >= 1
+    assert math.isfinite(baseline["value"]) and baseline["value"] > 0
