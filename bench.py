@@ -216,33 +216,19 @@ class PeakWorkload:
         # One host iteration = every chain's tile product of every sampled block.
         best = _best_of(lambda: ot.peak_reference(a, b, 1), CPU_ROW_BUDGET_S)
         flops = 2 * m * n * k * chains * blocks
-        return flops / best / 1e12, _blas_threads(), (
+        from triton_chip_benchmarks_amd.cpu_baseline import blas_threads
+
+        return flops / best / 1e12, blas_threads(), (
             f"oracle.tensor.peak_reference (numpy float64 matmul) of {blocks} blocks x {chains} chain(s) of "
             f"{m}x{n}x{k} tiles, best repeat within {CPU_ROW_BUDGET_S:g} s")
 
 
 def host_description(torch) -> dict:
-    """The host the CPU baseline ran on: model name, logical CPUs, usable CPUs, torch threads."""
-    model = None
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "usable_cpus": usable,
-            "torch_threads": torch.get_num_threads(), "blas_threads": _blas_threads()}
+    """The host the CPU baseline ran on (model, CPUs, torch and BLAS threads)."""
+    del torch
+    from triton_chip_benchmarks_amd.cpu_baseline import host_description as describe
 
-
-def _blas_threads():
-    try:
-        from threadpoolctl import threadpool_info
-
-        return max((pool.get("num_threads", 1) for pool in threadpool_info()), default=1)
-    except ImportError:
-        return os.cpu_count() or 1
+    return describe()
 
 
 def build_workloads(torch, selected, compute_units):

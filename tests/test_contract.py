@@ -393,3 +393,20 @@ def test_package_scripts_import_when_run_directly(script):
                                capture_output=True, text=True, timeout=120, check=False)
     assert completed.returncode == 0, completed.stderr[-2000:]
     assert "usage" in completed.stdout
+
+
+def test_measured_rows_carry_the_host_baseline_and_the_table_lists_it():
+    baseline = {"value": 1.5, "unit": "TFLOP/s", "cores": 16, "method": "torch.matmul on the host in float32",
+                "sample": "2048x2048x2048; best of 5 host runs", "host": {"cpu_model": "Test CPU"}}
+    document = {"status": "ok", "cpu_baseline": baseline,
+                "results": [{"status": "ok", "peak_teraops_per_second": 2000.0,
+                             "median_teraops_per_second": 1990.0,
+                             "compiled": {"execution_kind": "tensor", "native_tensor_verified": True,
+                                          "instruction_precision_verified": True}}]}
+    row = summarize(metric("tensor_bf16"), document)
+    assert row["status"] == "ok" and row["cpu_baseline"] == baseline
+    declared = summarize(metric("tensor_tf32"), {"status": "unsupported", "reason": "no xf32",
+                                                "cpu_baseline": baseline})
+    assert "cpu_baseline" not in declared
+    table = format_table([row, declared])
+    assert "Host CPU baseline" in table and "Test CPU" in table and "torch.matmul" in table

@@ -40,6 +40,8 @@ def test_quick_suite_runs_children_and_keeps_the_row_contract(gpu, tmp_path):
         assert rows[key]["status"] == "ok" and rows[key]["value"] > 0, rows[key]
         assert rows[key].get("smoke_only") is True
         assert Path(rows[key]["log_file"]).exists()
+        baseline = rows[key]["cpu_baseline"]  # the reference's host computation, timed beside the row
+        assert baseline["value"] > 0 and baseline["cores"] >= 1 and baseline["host"]["os_cpu_count"] >= 1
     fp8 = rows["vector_fp8"]
     assert fp8["status"] == "not_implemented" and fp8["value"] is None
     assert fp8["widened_measurement"]["peak_tflops"] > 0

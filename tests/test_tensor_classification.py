@@ -25,7 +25,7 @@ AUDITED = {"spill_count": 0, "register_spills": 0, "registers_per_thread": 64, "
 
 def _args(tmp_path, dtype="bf16"):
     parser = bt.build_parser()
-    args = parser.parse_args(["--dtype", dtype, "--blocks-per-sm", "1", "--iterations", "3",
+    args = parser.parse_args(["--dtype", dtype, "--blocks-per-sm", "1", "--iterations", "3", "--no-cpu-baseline",
                               "--output", str(tmp_path / "tensor.json")])
     bt.normalize_precision_args(parser, args)
     args.tiles = None
@@ -104,3 +104,13 @@ def test_spilling_configuration_is_skipped_and_the_invocation_fails(tmp_path, st
     with pytest.raises(RuntimeError, match="spills registers"):
         _run(tmp_path)
     assert stand_ins["timed"] == 0
+
+
+def test_measured_document_carries_the_host_matmul_baseline(tmp_path, stand_ins):
+    args = _args(tmp_path)
+    args.no_cpu_baseline, args.quick = False, True
+    bt.run_peak(args, {"sm_count": 2}, "cpu")
+    document = json.loads((tmp_path / "tensor.json").read_text())
+    baseline = document["cpu_baseline"]
+    assert baseline["unit"] == "TFLOP/s" and baseline["value"] > 0 and baseline["cores"] >= 1
+    assert "torch.matmul" in baseline["method"] and "256x256x256" in baseline["sample"]

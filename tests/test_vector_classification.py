@@ -27,7 +27,7 @@ NATIVE_FP32 = ["v_fma_f32 v0, v1, s2, v0"]
 def _args(tmp_path, dtype):
     parser = bv.build_parser()
     args = parser.parse_args(["--dtype", dtype, "--iterations", "8", "--blocks-per-sm", "1", "--block-sizes", "64",
-                              "--unroll", "1", "--output", str(tmp_path / "vector.json")])
+                              "--unroll", "1", "--no-cpu-baseline", "--output", str(tmp_path / "vector.json")])
     bv.configure_sweep(args)
     return args
 

@@ -17,11 +17,11 @@ import sys
 
 if __package__ in (None, ""):
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
-    from triton_chip_benchmarks_amd import _native, roofline
+    from triton_chip_benchmarks_amd import _native, cpu_baseline, roofline
     from triton_chip_benchmarks_amd.common import (add_common_arguments, available_memory_bytes, emit_results,
                                                    get_device, measure, positive_int, setup_device)
 else:
-    from . import _native, roofline
+    from . import _native, cpu_baseline, roofline
     from .common import (add_common_arguments, available_memory_bytes, emit_results, get_device, measure,
                          positive_int, setup_device)
 
@@ -290,7 +290,12 @@ def main(argv=None):
     if not eligible:
         print("No HBM-sized peak candidate: eligibility requires buffers >= 4x the last-level cache "
               "and a run without --quick.")
-    emit_results("bandwidth", metadata, args, rows)
+    baseline = None
+    if not args.no_cpu_baseline and "copy" in modes:
+        # The reference's host path for this row: a tensor copy (1 GiB; 64 MiB in smoke mode).
+        baseline = cpu_baseline.copy_baseline((64 if args.quick else 1024) * 2**20)
+        print(f"CPU baseline (host, {baseline['cores']} threads): {baseline['value']:.1f} GB/s copy")
+    emit_results("bandwidth", metadata, args, rows, cpu_baseline=baseline)
 
 
 if __name__ == "__main__":

@@ -20,11 +20,11 @@ import sys
 
 if __package__ in (None, ""):
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
-    from triton_chip_benchmarks_amd import _native, audit, formats, roofline
+    from triton_chip_benchmarks_amd import _native, audit, cpu_baseline, formats, roofline
     from triton_chip_benchmarks_amd.common import (add_common_arguments, available_memory_bytes, emit_results,
                                                    emit_unsupported, get_device, measure, setup_device)
 else:
-    from . import _native, audit, formats, roofline
+    from . import _native, audit, cpu_baseline, formats, roofline
     from .common import (add_common_arguments, available_memory_bytes, emit_results, emit_unsupported,
                          get_device, measure, setup_device)
 
@@ -425,7 +425,13 @@ def emit_tensor_results(metadata: dict, args, rows: list[dict]) -> None:
         frac = best["peak_teraops_per_second"] / roofline.PEAKS[f"tensor_{args.dtype}"][0]
         print(f"Measured {args.mode} {args.dtype}: {best['peak_teraops_per_second']:.2f} {unit} "
               f"({100 * frac:.1f}% of the MI355X dense peak; median {best['median_teraops_per_second']:.2f})")
-        emit_results("tensor", metadata, args, rows)
+        baseline = None
+        if not getattr(args, "no_cpu_baseline", False):
+            # The reference's host path for this row: torch.matmul in float32 (float64 for FP64).
+            baseline = cpu_baseline.matmul_baseline(args.dtype, 256 if args.quick else 2048)
+            print(f"CPU baseline (host, {baseline['cores']} threads): {baseline['value']:.4g} {baseline['unit']} "
+                  f"({baseline['method']}, {baseline['sample']})")
+        emit_results("tensor", metadata, args, rows, cpu_baseline=baseline)
         return
     if any(row.get("status") == "unsupported" for row in rows):
         reason = "; ".join(dict.fromkeys(row.get("reason", "unsupported") for row in rows))

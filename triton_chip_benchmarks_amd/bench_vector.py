@@ -21,12 +21,12 @@ import sys
 
 if __package__ in (None, ""):
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
-    from triton_chip_benchmarks_amd import _native, audit, formats, roofline
+    from triton_chip_benchmarks_amd import _native, audit, cpu_baseline, formats, roofline
     from triton_chip_benchmarks_amd.common import (add_common_arguments, available_memory_bytes,
                                                    emit_not_implemented, emit_results, emit_unsupported,
                                                    get_device, measure, positive_int, setup_device)
 else:
-    from . import _native, audit, formats, roofline
+    from . import _native, audit, cpu_baseline, formats, roofline
     from .common import (add_common_arguments, available_memory_bytes, emit_not_implemented, emit_results,
                          emit_unsupported, get_device, measure, positive_int, setup_device)
 
@@ -415,7 +415,13 @@ def run_benchmark(args, metadata):
           f"({100 * best[peak_key] / peak_value:.1f}% of {peak_value:.1f}; variant {best['variant']}, "
           f"blocks/CU={best['blocks_per_sm']}, block={best['block_size']}, unroll={best['unroll']})")
     name = f"vector_{dtype}_{best['variant']}"
-    emit_results(name, {**metadata, "vector_excluded_configurations": excluded}, args, rows)
+    baseline = None
+    if not args.no_cpu_baseline:
+        # The reference's host path for this row: the recurrence vectorised over the lane set.
+        baseline = cpu_baseline.vector_baseline(dtype, 2**16 if args.quick else 2**22, 2 if args.quick else 8)
+        print(f"CPU baseline (host, {baseline['cores']} threads): {baseline['value']:.4g} {baseline['unit']} "
+              f"({baseline['sample']})")
+    emit_results(name, {**metadata, "vector_excluded_configurations": excluded}, args, rows, cpu_baseline=baseline)
 
 
 # ---- widened (converted) FP8 / FP4 chains ----------------------------------------

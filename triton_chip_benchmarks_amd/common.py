@@ -56,6 +56,8 @@ def add_common_arguments(parser):
                         help="Last-level cache capacity in MiB for the HBM-sized buffer rule "
                              "(default: the MI355X 256 MiB Infinity Cache)")
     parser.add_argument("--output", type=Path, help="Save metadata and all samples as JSON")
+    parser.add_argument("--no-cpu-baseline", action="store_true",
+                        help="Skip timing the reference's host computation beside the device rate")
 
 
 def _torch():
@@ -349,7 +351,7 @@ def emit_not_implemented(name, metadata, args, reason, *, details=None):
     return _emit_no_measurement(name, metadata, args, reason, "not_implemented", details=details)
 
 
-def emit_results(name, metadata, args, rows):
+def emit_results(name, metadata, args, rows, *, cpu_baseline=None):
     if not rows:
         raise RuntimeError("No valid measurements were produced")
     methods = sorted({row["timing_method"] for row in rows if "timing_method" in row})
@@ -369,5 +371,7 @@ def emit_results(name, metadata, args, rows):
         },
         "results": rows,
     }
+    if cpu_baseline is not None:
+        document["cpu_baseline"] = cpu_baseline
     _write_document(args, document)
     return document

@@ -107,6 +107,15 @@ def _verification_reason(metric, details):
 
 
 def summarize(metric, document):
+    """One report row; a measured row also carries the child's host CPU baseline."""
+    result = _summarize(metric, document)
+    baseline = document.get("cpu_baseline")
+    if result.get("status") in ("ok", "unverified") and isinstance(baseline, dict):
+        result["cpu_baseline"] = baseline
+    return result
+
+
+def _summarize(metric, document):
     """One report row from a child's result document.
 
     A declared status (unsupported, not_implemented, error, unavailable) is
@@ -195,6 +204,15 @@ def format_table(results):
         if item.get("execution_kind") == "simt":
             notes.append(f"{item['metric']}: measured matrix rate using SIMT scalar/vector instructions "
                          "(no native tensor MMA)")
+    baselines = [item for item in results if isinstance(item.get("cpu_baseline"), dict)]
+    if baselines:
+        host = baselines[0]["cpu_baseline"].get("host") or {}
+        lines.extend(("", f"Host CPU baseline (the reference's host computation, {host.get('cpu_model') or 'CPU'}, "
+                          f"{baselines[0]['cpu_baseline'].get('cores')} threads):"))
+        for item in baselines:
+            baseline = item["cpu_baseline"]
+            lines.append(f"  {item['metric']:<20} {baseline['value']:>12.4g} {baseline['unit']:<8} "
+                         f"{baseline.get('method', '')}; {baseline.get('sample', '')}")
     if notes:
         lines.extend(("", *notes))
     return "\n".join(lines)
