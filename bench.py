@@ -1,81 +1,94 @@
 #!/usr/bin/env python3
 """Headline benchmark of the MI355X peak-throughput suite (one JSON line).
 
-Metric: "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of
-MI355X peak". One step is one pass of the hot path over resident synthetic
-inputs - one launch of each headline kernel:
-  hbm_copy    mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from seed 0) into a
-              second buffer (memory_bandwidth row);
-  peak_bf16   mb_tensor_peak BF16: the resident-operand variant that loops a
-              256x256x64 LDS tile 1024 times per workgroup, 2 workgroups per
-              CU (tensor_bf16 row);
-  peak_fp8    FP8 E4M3, 128x128x128 tiles, 2 chains, 1024 iterations, 4
-              workgroups per CU (tensor_fp8 row);
-  peak_mxfp4  MX FP4 E2M1 + E8M0 scales, 128x128x256 tiles, 2 chains, 1024
-              iterations, 4 workgroups per CU (tensor_fp4 row).
-Operands follow the reference's peak lattices (bench_tensor.py:614-672). Every
-kernel's output is validated before timing with the product's own checks
-(bit equality for the copy; exact float64 lattice references under the
-reference's tolerance for the MFMA rows).
+Metric: "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of MI355X
+peak". One step is one launch of every kernel below on inputs already resident
+in HBM. Each row is one configuration of the benchmark specification:
 
-Timing: for each kernel in turn, W untimed warmup launches, then its K timed
-launches back to back - captured once into a HIP graph and replayed - between
-two torch.cuda.synchronize() calls, as the reference's batch timing does
-(common.py:295-534). The output of the timed launches is checked again.
-MI355X raises its clock over ~40 ms when a matrix-bound kernel follows a
-memory-bound one, and the per-kernel warmup keeps that ramp out of the timed
-launches. A kernel's
-ms_per_launch is its batch time between two HIP events on the launch stream
-over K (no event between launches, as in the reference's event batches);
-ms_per_step is the sum of the kernels' batch times over K.
+  hbm_copy        configs[0]  mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from
+                              seed 0) into a second buffer; bit-exact
+  peak_bf16       configs[2]  resident-operand variant: a 256x256x64 BF16 LDS
+                              tile looped 1024 times per workgroup, 2 per CU
+  gemm_bf16       configs[2]  BF16 GEMM 8192^3, A, B ~ N(0,1), B column-major
+  gemm_fp16       configs[2]  FP16 GEMM 8192^3, same operands
+  gemm_fp8        configs[3]  FP8 E4M3 GEMM 8192^3 over {+-0.5, +-1, +-2}; exact
+  gemm_int8       configs[3]  INT8 GEMM 8192^3 over [-8, 8]; exact
+  gemm_fp64       configs[3]  FP64 GEMM 4096^3, N(0,1)
+  gemm_mxfp4      configs[4]  MXFP4 GEMM 16384^3, all 16 E2M1 codes, E8M0
+                              scale 127 per 32 K elements; exact
+  peak_fp8        17-row table: FP8 resident tile 128x128x128, 2 chains,
+                              the reference's one-hot operands
+  peak_fp8_dense  the same kernel on the dense {+-0.5, +-1, +-2} set
+  peak_mxfp4      17-row table: MXFP4 resident tile 128x128x256, 2 chains,
+                              the reference's +-0.5/+-1 codes
 
-value = mean over the headline rows of (achieved rate / MI355X published
-peak), in percent; the absolute rates are in "rows". The CPU baseline times
-the oracle (numpy) on bounded samples of the same work on the host.
+value = mean of achieved / MI355X published peak, in percent, over the
+HEADLINE rows (hbm_copy, peak_bf16, gemm_bf16, gemm_fp8, gemm_mxfp4: the
+metric's four formats at the specification's sizes); every row carries its
+own fraction. Every output is validated before timing and again on the timed
+launches' output (bit-exact copy; exact FP8/INT8/MXFP4 GEMMs; elementwise
+|C-R| <= atol + rtol*|R| for BF16/FP16 (1e-2) and FP64 (1e-12) against a
+float64 device product; the resident tiles against their exact lattice
+reference under the reference's tolerance).
+
+Timing, per kernel in turn (the reference's policy, common.py:459-461, warms
+for a device-time budget): untimed launches until at least --warmup launches
+AND --warmup-ms of device time have run, so the clock has settled at this
+kernel's load; then exactly --steps launches, bracketed by
+torch.cuda.synchronize(), with HIP events on the launch stream between
+sub-batches of about --sub-batch-ms. ms_per_launch is the whole timed region
+over --steps; min and median are over the sub-batch averages.
+
+cpu_baseline times the reference's own host arithmetic for each row on this
+machine's cores (torch.Tensor.copy_ of 1 GiB; torch.matmul in fp32, fp64
+for FP64, on sampled rows of the same GEMM shape or a batch of the same
+tiles), best repeat within a per-row budget.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 from pathlib import Path
+import statistics
 import sys
-import time
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "MFMA TFLOP/s (BF16/FP8/MXFP4) + HBM copy GB/s, as % of MI355X peak"
+HEADLINE = ("hbm_copy", "peak_bf16", "gemm_bf16", "gemm_fp8", "gemm_mxfp4")
 COPY_ELEMENTS = 2**28
 COPY_SEED = 0
-# Launch shapes chosen from the bench_bandwidth / bench_tensor sweeps on MI355X.
-# One 64-lane wave per workgroup, one 16-byte vector per lane: the fastest measured
-# shape on MI355X (more vectors per lane or larger workgroups lose 1-8%); streaming
-# policy: nt loads, device-scope stores written through the L2 (~1% over nt stores).
+# One 64-lane wave per workgroup, one 16-byte vector per lane, nt loads and
+# device-scope stores written through the L2: the fastest shape and policy of
+# the bench_bandwidth sweep on MI355X.
 COPY_CONFIG = {"block_threads": 64, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": "stream"}
 PEAK_ITERATIONS = 1024
-# (tile M, N, K, chains, workgroups per CU). BF16 is the headline resident
-# variant (256x256x64 tile); FP8 and MXFP4 use the fastest tiles of the bench_tensor sweep.
-PEAK_SHAPES = {"bf16": (256, 256, 64, 1, 2), "fp8": (128, 128, 128, 2, 4), "fp4": (128, 128, 256, 2, 4)}
+GEMM_SEED = 0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_per_launch.txt"
-CPU_ROW_BUDGET_S = 4.0  # host seconds per row: about 16 s of CPU work in all
+CPU_ROW_BUDGET_S = 2.0
 
 
 def parse_args(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--steps", type=int, default=50, help="timed launches of each kernel (default: 50)")
     parser.add_argument("--warmup", type=int, default=20,
-                        help="untimed launches of each kernel right before its timed ones (default: 20)")
-    parser.add_argument("--no-cpu-baseline", action="store_true",
-                        help="Skip the timed CPU baseline leg (it is on by default)")
-    parser.add_argument("--rows", nargs="+", help="Subset of headline rows: hbm_copy peak_bf16 peak_fp8 peak_mxfp4")
+                        help="minimum untimed launches of each kernel before its timed ones (default: 20)")
+    parser.add_argument("--warmup-ms", type=float, default=250.0,
+                        help="minimum device time of those untimed launches, per kernel (default: 250)")
+    parser.add_argument("--sub-batch-ms", type=float, default=2.0,
+                        help="device time between two events inside the timed launches (default: 2)")
+    parser.add_argument("--no-cpu-baseline", action="store_true", help="skip the host CPU leg")
+    parser.add_argument("--rows", nargs="+", help="subset of rows to run (default: all)")
     return parser.parse_args(argv)
 
 
 def traffic_table() -> dict[str, float]:
-    """Measured HBM bytes per launch by kernel (from committed rocprofv3 counter runs)."""
+    """Measured HBM bytes per launch by kernel name (committed rocprofv3 counter runs)."""
     table = {}
     if TRAFFIC_FILE.exists():
         for line in TRAFFIC_FILE.read_text().splitlines():
@@ -89,41 +102,49 @@ def traffic_table() -> dict[str, float]:
     return table
 
 
-def _best_of(fn, budget_s):
-    """Best wall time of repeated host calls within a time budget (CPU leg only)."""
-    fn()
-    best, spent = None, 0.0
-    while spent < budget_s or best is None:
-        start = time.perf_counter()
-        fn()
-        elapsed = time.perf_counter() - start
-        spent += elapsed
-        best = elapsed if best is None else min(best, elapsed)
-    return best
+class Workload:
+    """One row: owns its resident device buffers; launch() enqueues one kernel launch."""
 
-
-class CopyWorkload:
-    """memory_bandwidth row: 1 GiB fp32 device-to-device copy."""
-
-    name, dtype, metric_key, unit, bound = "hbm_copy", "f32", "memory_bandwidth", "GB/s", "hbm"
-
-    def __init__(self, torch):
-        from triton_chip_benchmarks_amd import bench_bandwidth
-
-        self.torch = torch
-        self.launcher = bench_bandwidth.launch_copy
-        generator = torch.Generator(device="cuda")
-        generator.manual_seed(COPY_SEED)
-        self.src = torch.empty(COPY_ELEMENTS, device="cuda", dtype=torch.float32).uniform_(-1, 1, generator=generator)
-        self.dst = torch.empty_like(self.src)
-        self.work = 2 * self.src.numel() * 4  # algorithmic bytes: read + write (bench_bandwidth.py:212)
-        self.kernel = f"copy_dwordx4_vpt{COPY_CONFIG['vectors_per_thread']}" + bench_bandwidth.POLICY_SUFFIX[
-            bench_bandwidth.copy_policy(COPY_CONFIG["nontemporal"])]
-        self.config = {"elements": COPY_ELEMENTS, "dtype": "fp32", **COPY_CONFIG}
+    name = row = unit = bound = label = kernel = ""
+    work = 0.0
+    config: dict = {}
 
     def launch(self):
-        self.launcher(self.src, self.dst, COPY_CONFIG["block_threads"], COPY_CONFIG["vectors_per_thread"],
-                      COPY_CONFIG["grid_blocks"], COPY_CONFIG["nontemporal"])
+        raise NotImplementedError
+
+    def poison(self):
+        raise NotImplementedError
+
+    def check(self) -> str:
+        raise NotImplementedError
+
+    def cpu(self) -> dict:
+        raise NotImplementedError
+
+    def rate(self, ms: float) -> float:
+        return self.work / (ms * (1e6 if self.unit == "GB/s" else 1e9))
+
+
+class CopyWorkload(Workload):
+    name, row, unit, bound, label = "hbm_copy", "memory_bandwidth", "GB/s", "hbm", "f32 copy"
+
+    def __init__(self, torch, compute_units):
+        from triton_chip_benchmarks_amd import bench_bandwidth
+
+        del compute_units
+        self.torch, self.bb = torch, bench_bandwidth
+        generator = torch.Generator(device="cuda").manual_seed(COPY_SEED)
+        self.src = torch.empty(COPY_ELEMENTS, device="cuda", dtype=torch.float32).uniform_(-1, 1, generator=generator)
+        self.dst = torch.empty_like(self.src)
+        self.work = 2 * self.src.numel() * 4  # read + write bytes (bench_bandwidth.py:212)
+        self.kernel = f"copy_dwordx4_vpt{COPY_CONFIG['vectors_per_thread']}" + bench_bandwidth.POLICY_SUFFIX[
+            bench_bandwidth.copy_policy(COPY_CONFIG["nontemporal"])]
+        self.config = {"elements": COPY_ELEMENTS, "dtype": "fp32", "seed": COPY_SEED, **COPY_CONFIG}
+
+    def launch(self):
+        c = COPY_CONFIG
+        self.bb.launch_copy(self.src, self.dst, c["block_threads"], c["vectors_per_thread"], c["grid_blocks"],
+                            c["nontemporal"])
 
     def poison(self):
         self.dst.fill_(float("nan"))
@@ -131,126 +152,212 @@ class CopyWorkload:
     def check(self):
         self.torch.cuda.synchronize()
         if not self.torch.equal(self.src.view(self.torch.int32), self.dst.view(self.torch.int32)):
-            raise AssertionError("copy output differs from its source")
+            raise AssertionError("hbm_copy: destination differs from its source")
         return "bit-exact: every word of the 1 GiB destination equals the source"
 
-    def validate(self):
-        self.poison()
-        self.launch()
-        return self.check()
+    def cpu(self):
+        from triton_chip_benchmarks_amd import cpu_baseline
 
-    def rate(self, ms):
-        return self.work / (ms * 1e6)  # GB/s
-
-    def cpu_rate(self):
-        """oracle.memory.copy of a 256 MiB host sample."""
-        import numpy as np
-
-        from oracle import memory
-
-        sample = np.random.default_rng(COPY_SEED).uniform(-1, 1, size=2**26).astype(np.float32)
-        best = _best_of(lambda: memory.copy(sample), CPU_ROW_BUDGET_S)
-        return 2 * sample.nbytes / best / 1e9, 1, "oracle.memory.copy (numpy) of 2^26 fp32 (256 MiB)"
+        return cpu_baseline.copy_baseline(COPY_ELEMENTS * 4, CPU_ROW_BUDGET_S)
 
 
-class PeakWorkload:
-    """tensor_<dtype> row: resident-operand MFMA peak kernel."""
+class PeakWorkload(Workload):
+    """A resident-operand MFMA tile looped PEAK_ITERATIONS times per workgroup (tensor rows)."""
 
     unit, bound = "TFLOP/s", "mfma"
+    LABELS = {"bf16": "bf16", "fp8": "fp8_e4m3", "fp4": "mxfp4_e2m1"}
 
-    def __init__(self, torch, dtype, compute_units):
+    def __init__(self, torch, compute_units, name, dtype, tile, chains, per_cu, operands="lattice"):
         from triton_chip_benchmarks_amd import _native, bench_tensor
 
-        self.torch, self.bt, self.dtype = torch, bench_tensor, dtype
-        self.name = "peak_mxfp4" if dtype == "fp4" else f"peak_{dtype}"
-        self.metric_key = f"tensor_{dtype}"
-        m, n, k, chains, per_cu = PEAK_SHAPES[dtype]
-        blocks = per_cu * compute_units
-        self.config = next(c for c in _native.peak_configs(dtype)
-                           if (c["tile_m"], c["tile_n"], c["tile_k"]) == (m, n, k) and c["chains"] == chains
-                           and not c["b_nk"])
-        self.kernel = _native.peak_kernel_name(dtype, self.config)
-        self.blocks = blocks
+        self.torch, self.bt, self.dtype, self.name = torch, bench_tensor, dtype, name
+        self.row, self.label = f"tensor_{dtype}", self.LABELS[dtype]
+        m, n, k = tile
+        self.cfg = next(c for c in _native.peak_configs(dtype) if (c["tile_m"], c["tile_n"], c["tile_k"]) == tile
+                        and c["chains"] == chains and not c["b_nk"])
+        self.kernel = _native.peak_kernel_name(dtype, self.cfg)
+        self.blocks = per_cu * compute_units
         if dtype == "fp4":
-            self.a, self.b, self.c, self.scales, self.values = bench_tensor.fp4_peak_inputs(blocks, self.config, "cuda")
+            self.a, self.b, self.c, self.scales, self.values = bench_tensor.fp4_peak_inputs(self.blocks, self.cfg,
+                                                                                           "cuda")
+            operand_text = "codes of +-0.5 and +-1 (the reference's set), E8M0 scale 127"
         else:
-            self.a, self.b, self.c, b_logical = bench_tensor.peak_inputs(blocks, self.config, dtype, "cuda")
+            self.a, self.b, self.c, b_logical = bench_tensor.peak_inputs(self.blocks, self.cfg, dtype, "cuda",
+                                                                          operands=operands)
             self.scales, self.values = None, (self.a, b_logical)
-        self.work = 2 * m * n * k * PEAK_ITERATIONS * self.config["chains"] * blocks  # bench_tensor.py:1242
-        self.dtype_label = {"bf16": "bf16", "fp8": "fp8_e4m3", "fp4": "mxfp4_e2m1"}[dtype]
-        self.config_summary = {"tile": f"{m}x{n}x{k}", "chains": self.config["chains"], "blocks": blocks,
-                               "blocks_per_cu": per_cu, "iterations": PEAK_ITERATIONS, "b_layout": "kn"}
+            operand_text = {"lattice": "the reference's exact lattice" + (" (one-hot A)" if dtype == "fp8" else ""),
+                            "dense": "every entry from {+-0.5, +-1, +-2}"}[operands]
+        self.reference = bench_tensor.exact_reference(self.values[0], self.values[1], PEAK_ITERATIONS,
+                                                      torch.float32)
+        self.work = 2 * m * n * k * PEAK_ITERATIONS * chains * self.blocks  # bench_tensor.py:1242
+        self.config = {"tile": f"{m}x{n}x{k}", "chains": chains, "blocks": self.blocks, "blocks_per_cu": per_cu,
+                       "iterations": PEAK_ITERATIONS, "b_layout": "kn", "operands": operand_text}
 
     def launch(self):
-        self.bt.launch_peak(self.dtype, self.config, self.a, self.b, self.c, PEAK_ITERATIONS, self.scales)
+        self.bt.launch_peak(self.dtype, self.cfg, self.a, self.b, self.c, PEAK_ITERATIONS, self.scales)
 
     def poison(self):
         self.c.fill_(float("nan"))
 
     def check(self):
-        reference = self.bt.exact_reference(self.values[0], self.values[1], PEAK_ITERATIONS, self.torch.float32)
         self.torch.cuda.synchronize()
-        result = self.bt.validate_peak(self.c, reference, self.dtype, self.config["tile_k"], PEAK_ITERATIONS)
-        return (f"every output within atol {result['atol']:.3g} of the exact float64 lattice reference "
+        result = self.bt.validate_peak(self.c, self.reference, self.dtype, self.cfg["tile_k"], PEAK_ITERATIONS)
+        return (f"every output within atol {result['atol']:.3g} of the exact lattice reference "
                 f"(max error {result['max_abs_error']:.3g})")
 
-    def validate(self):
-        self.poison()
-        self.launch()
-        return self.check()
+    def cpu(self):
+        from triton_chip_benchmarks_amd import cpu_baseline
 
-    def rate(self, ms):
-        return self.work / (ms * 1e9)  # TFLOP/s
-
-    def cpu_rate(self):
-        """The same tile products on the host: oracle.tensor.peak_reference over a block sample."""
-        import numpy as np
-
-        from oracle import tensor as ot
-
-        m, n, k, chains, _ = PEAK_SHAPES[self.dtype]
-        rng = np.random.default_rng(0)
-        blocks = 64
-        a = ot.ternary_lattice(rng, (blocks, m, k))
-        b = ot.ternary_lattice(rng, (chains, blocks, k, n))
-        # One host iteration = every chain's tile product of every sampled block.
-        best = _best_of(lambda: ot.peak_reference(a, b, 1), CPU_ROW_BUDGET_S)
-        flops = 2 * m * n * k * chains * blocks
-        from triton_chip_benchmarks_amd.cpu_baseline import blas_threads
-
-        return flops / best / 1e12, blas_threads(), (
-            f"oracle.tensor.peak_reference (numpy float64 matmul) of {blocks} blocks x {chains} chain(s) of "
-            f"{m}x{n}x{k} tiles, best repeat within {CPU_ROW_BUDGET_S:g} s")
+        m, n, k = self.cfg["tile_m"], self.cfg["tile_n"], self.cfg["tile_k"]
+        return cpu_baseline.tile_batch_baseline(self.dtype, 64, m, n, k, CPU_ROW_BUDGET_S)
 
 
-def host_description(torch) -> dict:
-    """The host the CPU baseline ran on (model, CPUs, torch and BLAS threads)."""
-    del torch
-    from triton_chip_benchmarks_amd.cpu_baseline import host_description as describe
+class GemmWorkload(Workload):
+    """C = A . B at the specification's size (B column-major), largest tile of mb_gemm."""
 
-    return describe()
+    bound = "mfma"
+    LABELS = {"bf16": "bf16", "fp16": "fp16", "fp8": "fp8_e4m3", "int8": "int8", "fp64": "f64",
+              "fp4": "mxfp4_e2m1"}
+
+    def __init__(self, torch, compute_units, name, dtype, size):
+        from triton_chip_benchmarks_amd import _native, gemm
+
+        del compute_units
+        self.torch, self.gemm, self.native, self.dtype, self.name, self.size = torch, gemm, _native, dtype, name, size
+        self.row, self.label = f"tensor_{dtype}", self.LABELS[dtype]
+        self.unit = "TOP/s" if dtype == "int8" else "TFLOP/s"
+        self.cfg = max(_native.gemm_configs(dtype), key=lambda c: c["tile_m"] * c["tile_n"])
+        self.kernel = _native.gemm_kernel_name(dtype, self.cfg)
+        a, b, c, scales, a_values, b_values = gemm.gemm_inputs(dtype, size, size, size, "cuda", GEMM_SEED)
+        self.a, self.b, self.c, self.scales = a, b, c, scales or (None, None)
+        self.reference = gemm.reference(a_values, b_values)
+        del a_values, b_values
+        self.work = 2 * size**3
+        self.config = {"m": size, "n": size, "k": size, "tile": f"{self.cfg['tile_m']}x{self.cfg['tile_n']}x"
+                       f"{self.cfg['tile_k']}", "layout": "A row-major, B column-major",
+                       "operands": gemm.INPUT_PATTERN[dtype], "seed": GEMM_SEED}
+
+    def launch(self):
+        self.native.gemm(self.dtype, self.cfg, self.a, self.b, self.c, self.size, self.size, self.size, *self.scales)
+
+    def poison(self):
+        self.c.fill_(-2**31 if self.dtype == "int8" else float("nan"))
+
+    def check(self):
+        self.torch.cuda.synchronize()
+        result = self.gemm.validate(self.c, self.reference, self.dtype)
+        if result["rtol"]:
+            return (f"every entry within |C-R| <= {result['atol']:g} + {result['rtol']:g}*|R| of the float64 "
+                    f"product (max error {result['max_abs_error']:.3g}, worst error/allowed "
+                    f"{result['max_error_over_allowed']:.3g})")
+        return "bit-exact against the float64 product (the operand set is exact in the accumulator)"
+
+    def cpu(self):
+        from triton_chip_benchmarks_amd import cpu_baseline
+
+        rows = 256 if self.size <= 8192 else 128
+        return cpu_baseline.gemm_sample_baseline(self.dtype, rows, self.size, self.size, CPU_ROW_BUDGET_S)
 
 
-def build_workloads(torch, selected, compute_units):
-    workloads = [CopyWorkload(torch)] + [PeakWorkload(torch, d, compute_units) for d in ("bf16", "fp8", "fp4")]
-    if selected:
-        unknown = set(selected) - {w.name for w in workloads}
-        if unknown:
-            raise SystemExit(f"unknown rows: {', '.join(sorted(unknown))}")
-        workloads = [w for w in workloads if w.name in selected]
-    return workloads
+def _row_specs():
+    """(name, factory) in run order; factories take (torch, compute_units)."""
+    def peak(name, dtype, tile, chains, per_cu, operands="lattice"):
+        return name, lambda t, cu: PeakWorkload(t, cu, name, dtype, tile, chains, per_cu, operands)
+
+    def gemm(name, dtype, size):
+        return name, lambda t, cu: GemmWorkload(t, cu, name, dtype, size)
+
+    return [
+        ("hbm_copy", CopyWorkload),
+        peak("peak_bf16", "bf16", (256, 256, 64), 1, 2),
+        gemm("gemm_bf16", "bf16", 8192),
+        gemm("gemm_fp16", "fp16", 8192),
+        gemm("gemm_fp8", "fp8", 8192),
+        gemm("gemm_int8", "int8", 8192),
+        gemm("gemm_fp64", "fp64", 4096),
+        gemm("gemm_mxfp4", "fp4", 16384),
+        peak("peak_fp8", "fp8", (128, 128, 128), 2, 4),
+        peak("peak_fp8_dense", "fp8", (128, 128, 128), 2, 4, "dense"),
+        peak("peak_mxfp4", "fp4", (128, 128, 256), 2, 4),
+    ]
+
+
+class _Events:
+    def __init__(self, torch, stream):
+        self.torch, self.stream, self.marks = torch, stream, []
+
+    def mark(self, launches_so_far):
+        event = self.torch.cuda.Event(enable_timing=True)
+        event.record(self.stream)
+        self.marks.append((launches_so_far, event))
+
+    def intervals(self):
+        """[(launches, ms)] between consecutive marks (call after synchronize)."""
+        out = []
+        for (n0, e0), (n1, e1) in zip(self.marks, self.marks[1:]):
+            ms = float(e0.elapsed_time(e1))
+            if not math.isfinite(ms) or ms <= 0:
+                raise RuntimeError(f"invalid device event time {ms!r} ms")
+            out.append((n1 - n0, ms))
+        return out
+
+
+def warm(torch, stream, workload, min_launches, min_ms):
+    """Untimed launches until both minimums are met; returns (launches, device ms)."""
+    events = _Events(torch, stream)
+    events.mark(0)
+    workload.launch()
+    events.mark(1)
+    torch.cuda.synchronize()
+    first = events.intervals()[0][1]
+    done, elapsed, estimate = 1, first, first
+    # Submit ~50 ms of launches at a time and re-measure, until both minimums hold.
+    while done < min_launches or elapsed < min_ms:
+        chunk = max(1, min(math.ceil(50.0 / estimate), math.ceil(max(min_ms - elapsed, 0.0) / estimate)),
+                    min_launches - done)
+        events = _Events(torch, stream)
+        events.mark(0)
+        for _ in range(chunk):
+            workload.launch()
+        events.mark(chunk)
+        torch.cuda.synchronize()
+        ms = events.intervals()[0][1]
+        done, elapsed, estimate = done + chunk, elapsed + ms, ms / chunk
+    return done, elapsed, estimate
+
+
+def time_launches(torch, stream, workload, steps, per_batch):
+    """Exactly `steps` launches, an event after every `per_batch`; returns [(launches, ms)]."""
+    events = _Events(torch, stream)
+    torch.cuda.synchronize()
+    events.mark(0)
+    for index in range(1, steps + 1):
+        workload.launch()
+        if index % per_batch == 0 or index == steps:
+            events.mark(index)
+    torch.cuda.synchronize()
+    return events.intervals()
 
 
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported. Every headline kernel runs "
-              "on a single GPU, and a multi-GPU figure would be the sum of independent per-GPU rates, which "
-              "this build does not launch.", file=sys.stderr)
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported. Every row runs on a single "
+              "GPU; a multi-GPU figure would be the sum of independent per-GPU rates, which this build does not "
+              "launch.", file=sys.stderr)
         return 2
-    if args.steps <= 0 or args.warmup < 0:
-        print("--steps must be positive and --warmup non-negative", file=sys.stderr)
+    if args.steps <= 0 or args.warmup < 0 or args.warmup_ms < 0 or args.sub_batch_ms <= 0:
+        print("--steps and --sub-batch-ms must be positive, --warmup and --warmup-ms non-negative",
+              file=sys.stderr)
         return 2
+    specs = _row_specs()
+    if args.rows:
+        unknown = set(args.rows) - {name for name, _ in specs}
+        if unknown:
+            print(f"unknown rows: {', '.join(sorted(unknown))}", file=sys.stderr)
+            return 2
+        specs = [(name, factory) for name, factory in specs if name in args.rows]
+
     import torch
 
     from triton_chip_benchmarks_amd import _native, roofline
@@ -258,93 +365,84 @@ def main(argv=None):
 
     require_gpu(0)
     info = _native.device_query(0)
-    workloads = build_workloads(torch, args.rows, info["compute_units"])
-    checks = {w.name: w.validate() for w in workloads}
-
     stream = torch.cuda.current_stream()
-    batch_ms, timing_modes = [], []
-    for w in workloads:
-        # W untimed warmup launches right before the kernel's K timed ones, so
-        # the clock has settled at this kernel's load when timing starts.
-        for _ in range(args.warmup):
-            w.launch()
-        torch.cuda.synchronize()
-        # The K launches are captured once into a HIP graph and replayed, as the
-        # reference's event batches are (common.py:311-361); without graph
-        # support they are launched directly.
-        submit, mode = None, "hip_graph"
-        try:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for _ in range(args.steps):
-                    w.launch()
-            graph.replay()  # untimed: the first replay uploads the graph
-            torch.cuda.synchronize()
-            submit = graph.replay
-        except RuntimeError:
-            torch.cuda.synchronize()
-            mode = "direct_launches"
-
-            def submit(w=w):
-                for _ in range(args.steps):
-                    w.launch()
-        w.poison()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        submit()
-        end.record(stream)
-        torch.cuda.synchronize()
-        batch_ms.append(start.elapsed_time(end))
-        timing_modes.append(mode)
-        w.check()  # raises if the timed launches' output is wrong
-        checks[w.name] += "; the same check passed again on the timed launches' output"
-    total_ms = sum(batch_ms)
-
     traffic = traffic_table()
-    rows = []
-    for index, w in enumerate(workloads):
-        average = batch_ms[index] / args.steps
-        achieved = w.rate(average)
-        peak, _unit, basis = roofline.PEAKS[w.metric_key]
-        rows.append({"row": w.metric_key, "name": w.name, "kernel": w.kernel, "value": achieved, "unit": w.unit,
-                     "ms_per_launch": average, "peak": peak, "frac": achieved / peak,
-                     "peak_basis": basis, "bound": w.bound, "algorithmic_work_per_launch": w.work,
-                     "work_unit": "bytes" if w.bound == "hbm" else "flop",
-                     "traffic_bytes_per_launch": traffic.get(w.kernel),
-                     "config": getattr(w, "config_summary", None) or w.config, "validation": checks[w.name]})
-    value = 100.0 * sum(row["frac"] for row in rows) / len(rows)
-    dominant = max(rows, key=lambda row: row["ms_per_launch"])
-    roofline_block = {"bound": dominant["bound"], "kernel": dominant["kernel"], "row": dominant["row"],
+    rows, workloads = [], []
+    for name, factory in specs:
+        print(f"[bench] {name}: building operands and validating", file=sys.stderr, flush=True)
+        workload = factory(torch, info["compute_units"])
+        workload.poison()
+        workload.launch()
+        validation = workload.check()
+        workloads.append((workload, validation))
+
+    for workload, validation in workloads:
+        print(f"[bench] {workload.name}: warmup and {args.steps} timed launches", file=sys.stderr, flush=True)
+        warm_launches, warm_ms, estimate = warm(torch, stream, workload, args.warmup, args.warmup_ms)
+        per_batch = max(1, min(args.steps, round(args.sub_batch_ms / estimate)))
+        workload.poison()  # the timed launches must rewrite the whole output
+        samples = time_launches(torch, stream, workload, args.steps, per_batch)
+        workload.check()  # raises if the timed launches' output is wrong
+        validation += "; passed again on the timed launches' output"
+        total_ms = sum(ms for _, ms in samples)
+        per_launch = [ms / n for n, ms in samples]
+        mean_ms = total_ms / args.steps
+        achieved = workload.rate(mean_ms)
+        peak, _unit, basis = roofline.PEAKS[workload.row]
+        rows.append({
+            "name": workload.name, "row": workload.row, "in_headline": workload.name in HEADLINE,
+            "kernel": workload.kernel, "value": achieved, "unit": workload.unit, "peak": peak,
+            "frac": achieved / peak, "peak_basis": basis, "bound": workload.bound,
+            "ms_per_launch": mean_ms, "min_ms_per_launch": min(per_launch),
+            "median_ms_per_launch": statistics.median(per_launch),
+            "value_at_min": workload.rate(min(per_launch)), "value_at_median": workload.rate(statistics.median(per_launch)),
+            "sub_batches": len(samples), "launches_per_sub_batch": per_batch,
+            "warmup_launches": warm_launches, "warmup_device_ms": warm_ms,
+            "algorithmic_work_per_launch": workload.work, "work_unit": "bytes" if workload.bound == "hbm" else "flop",
+            "traffic_bytes_per_launch": traffic.get(workload.kernel), "dtype": workload.label,
+            "config": workload.config, "validation": validation})
+
+    headline = [r for r in rows if r["in_headline"]] or rows
+    value = 100.0 * sum(r["frac"] for r in headline) / len(headline)
+    dominant = max(headline, key=lambda r: r["ms_per_launch"])
+    roofline_block = {"bound": dominant["bound"], "kernel": dominant["kernel"], "row": dominant["name"],
                       "achieved": dominant["value"], "peak": dominant["peak"], "unit": dominant["unit"],
                       "frac": dominant["frac"], "traffic": dominant["traffic_bytes_per_launch"],
                       "algorithmic_work_per_launch": dominant["algorithmic_work_per_launch"],
                       "ms_per_launch": dominant["ms_per_launch"]}
     cpu = None
     if not args.no_cpu_baseline:
+        from triton_chip_benchmarks_amd.cpu_baseline import host_description
+
         cpu_rows = []
-        for w in workloads:
-            cpu_value, cores, sample = w.cpu_rate()
-            peak = roofline.PEAKS[w.metric_key][0]
-            cpu_rows.append({"row": w.metric_key, "value": cpu_value, "unit": w.unit, "cores": cores,
-                             "sample": sample, "frac_of_mi355x_peak": cpu_value / peak})
-        cpu = {"value": 100.0 * sum(r["frac_of_mi355x_peak"] for r in cpu_rows) / len(cpu_rows),
-               "unit": "% of MI355X peak (mean over headline rows)",
-               "cores": max(r["cores"] for r in cpu_rows), "kind": "port",
-               "sample": "; ".join(f"{r['row']}: {r['sample']}" for r in cpu_rows),
-               "host_cpu_count": os.cpu_count(), "host": host_description(torch), "rows": cpu_rows}
+        for workload, _ in workloads:
+            print(f"[bench] {workload.name}: host CPU baseline", file=sys.stderr, flush=True)
+            result = workload.cpu()
+            peak = roofline.PEAKS[workload.row][0]
+            cpu_rows.append({"name": workload.name, "value": result["value"], "unit": result["unit"],
+                             "cores": result["cores"], "method": result["method"], "sample": result["sample"],
+                             "frac_of_mi355x_peak": result["value"] / peak})
+        in_mean = [r for r in cpu_rows if r["name"] in HEADLINE] or cpu_rows
+        cpu = {"value": 100.0 * sum(r["frac_of_mi355x_peak"] for r in in_mean) / len(in_mean),
+               "unit": "% of MI355X peak (mean over the headline rows)", "cores": max(r["cores"] for r in cpu_rows),
+               "kind": "port",
+               "sample": "; ".join(f"{r['name']}: {r['method']}, {r['sample']}" for r in cpu_rows),
+               "host": host_description(), "rows": cpu_rows}
     line = {
-        "metric": METRIC, "value": value, "unit": "% of MI355X peak (mean over headline rows)",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": total_ms / args.steps,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": ",".join(getattr(w, "dtype_label", w.dtype) for w in workloads),
-        "data": "synthetic: seeded uniform fp32 copy source; exact-lattice MFMA operands, resident in HBM",
-        "config": {"workload": " + ".join(w.name for w in workloads), "device": info["name"], "arch": info["arch"],
-                   "compute_units": info["compute_units"], "peak_iterations": PEAK_ITERATIONS,
-                   "copy_elements": COPY_ELEMENTS,
-                   "timing": "per kernel: W warmup launches, then K launches replayed from one HIP graph "
-                             "between two HIP events" if all(m == "hip_graph" for m in timing_modes)
-                             else "per kernel: W warmup launches, then K direct launches between two HIP events"},
+        "metric": METRIC, "value": value, "unit": "% of MI355X peak (mean over the headline rows)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": sum(r["ms_per_launch"] for r in rows), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": ",".join(dict.fromkeys(r["dtype"] for r in headline)),
+        "data": "synthetic, seeded, resident in HBM: uniform fp32 copy source; N(0,1) BF16/FP16/FP64 GEMM "
+                "operands; exact FP8/INT8/MXFP4 GEMM sets; exact lattices for the resident tiles",
+        "config": {"workload": "mean over " + " + ".join(r["name"] for r in headline)
+                   + ("; also reported: " + ", ".join(r["name"] for r in rows if not r["in_headline"])
+                      if any(not r["in_headline"] for r in rows) else ""),
+                   "device": info["name"], "arch": info["arch"], "compute_units": info["compute_units"],
+                   "warmup_ms_per_kernel": args.warmup_ms, "sub_batch_ms": args.sub_batch_ms,
+                   "timing": "per kernel: untimed launches for >= warmup launches and >= warmup_ms, then exactly "
+                             "`steps` launches with HIP events on the launch stream between sub-batches"},
         "roofline": roofline_block, "cpu_baseline": cpu, "rows": rows,
     }
     print(json.dumps(line))

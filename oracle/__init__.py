@@ -21,5 +21,8 @@ How each part is pinned (checks that a plausible mistake would fail):
   tensor   - float64 matmul on exact lattices (a library routine), the
              reference's tolerance/op-count golden values, the E2M1 table and
              packing known answers, FP8 E4M3FN decoding against torch's
-             float8_e4m3fn, E8M0 scale doubling.
+             float8_e4m3fn, E8M0 scale doubling; the elementwise GEMM rule
+             against torch.testing.assert_close and known answers a normwise
+             rule would get wrong; the FP32/FP64 probe operands against the
+             TF32/BF16/FP16/FP32 roundings they must expose.
 """

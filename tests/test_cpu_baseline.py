@@ -42,6 +42,17 @@ def test_matmul_baseline_uses_the_references_check_arithmetic(dtype, unit):
     assert ("upcast" in result["method"]) == (dtype not in ("fp32", "fp64"))
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp64", "fp4"])
+def test_gemm_sample_and_tile_batch_baselines(dtype):
+    result = cpu_baseline.gemm_sample_baseline(dtype, 16, 96, 64, budget_s=0.05)
+    _check(result, "TFLOP/s")
+    assert "16x96x64 (rows of A sampled)" in result["sample"]
+    assert ("float64" in result["method"]) == (dtype == "fp64")
+    tiles = cpu_baseline.tile_batch_baseline(dtype, 4, 32, 32, 16, budget_s=0.05)
+    _check(tiles, "TFLOP/s")
+    assert "4 tiles of 32x32x16" in tiles["sample"]
+
+
 @pytest.mark.parametrize("dtype,unit", [("fp32", "TFLOP/s"), ("fp64", "TFLOP/s"), ("fp16", "TFLOP/s"),
                                         ("bf16", "TFLOP/s"), ("int8", "TOPS")])
 def test_vector_baseline_runs_every_format(dtype, unit):

@@ -1,8 +1,9 @@
 """GPU test of the headline line's contract: one JSON line with every field the
 driver reads, a roofline block for the dominant kernel and a CPU baseline.
 
-The run is short (2 timed launches per kernel after 1 warmup) and exercises
-the same code path as the default run.
+The run is short (2 timed launches per kernel after a 30 ms warmup) and
+exercises the same code path as the default run: every row of the
+benchmark specification, validated before and after timing.
 """
 
 import json
@@ -21,7 +22,8 @@ TOP_LEVEL = {"metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_ste
 
 
 def test_bench_prints_one_contract_line(gpu):
-    completed = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--steps", "2", "--warmup", "1"],
+    completed = subprocess.run([sys.executable, "-u", str(ROOT / "bench.py"), "--steps", "2", "--warmup", "1",
+                                "--warmup-ms", "30"],
                                cwd=ROOT, capture_output=True, text=True, timeout=600, check=False)
     assert completed.returncode == 0, completed.stderr[-3000:]
     lines = [line for line in completed.stdout.splitlines() if line.strip()]
@@ -33,16 +35,23 @@ def test_bench_prints_one_contract_line(gpu):
     assert line["higher_is_better"] is True and line["vs_baseline"] is None
     assert "workload" in line["config"] and "model" not in line["config"]
     rows = {row["name"]: row for row in line["rows"]}
-    assert set(rows) == {"hbm_copy", "peak_bf16", "peak_fp8", "peak_mxfp4"}
-    fractions = [row["frac"] for row in rows.values()]
-    assert all(0.3 < frac < 1.0 for frac in fractions), fractions
+    assert set(rows) == {"hbm_copy", "peak_bf16", "gemm_bf16", "gemm_fp16", "gemm_fp8", "gemm_int8", "gemm_fp64",
+                         "gemm_mxfp4", "peak_fp8", "peak_fp8_dense", "peak_mxfp4"}
+    headline = {name for name, row in rows.items() if row["in_headline"]}
+    assert headline == {"hbm_copy", "peak_bf16", "gemm_bf16", "gemm_fp8", "gemm_mxfp4"}
+    assert all(name in line["config"]["workload"] for name in rows)
+    fractions = [rows[name]["frac"] for name in headline]
+    assert all(0.2 < row["frac"] < 1.0 for row in rows.values()), {n: r["frac"] for n, r in rows.items()}
     assert line["value"] == pytest.approx(100 * sum(fractions) / len(fractions))
     assert line["ms_per_step"] == pytest.approx(sum(row["ms_per_launch"] for row in rows.values()))
+    for row in rows.values():
+        assert row["min_ms_per_launch"] <= row["median_ms_per_launch"] * (1 + 1e-9)
+        assert row["warmup_device_ms"] >= 30 * 0.99 and "timed launches" in row["validation"]
     roofline = line["roofline"]
     assert {"bound", "achieved", "peak", "unit", "frac", "traffic"} <= set(roofline)
     assert roofline["bound"] in ("hbm", "mfma")
     assert roofline["frac"] == pytest.approx(roofline["achieved"] / roofline["peak"])
-    dominant = max(rows.values(), key=lambda row: row["ms_per_launch"])
+    dominant = max((rows[name] for name in headline), key=lambda row: row["ms_per_launch"])
     assert roofline["kernel"] == dominant["kernel"]
     baseline = line["cpu_baseline"]
     assert {"value", "unit", "cores", "kind", "sample"} <= set(baseline)

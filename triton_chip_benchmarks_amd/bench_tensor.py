@@ -126,18 +126,31 @@ def _generator(device, seed):
     return generator
 
 
-def peak_inputs(blocks: int, config: dict, dtype: str, device, seed: int = 0):
+FP8_DENSE_SET = (-2.0, -1.0, -0.5, 0.5, 1.0, 2.0)
+
+
+def peak_inputs(blocks: int, config: dict, dtype: str, device, seed: int = 0, operands: str = "lattice"):
     """Exact-lattice operands (bench_tensor.py:647-672) in the kernel's layouts.
 
     Returns (a, b, c, b_logical): b is stored [chains, blocks, K, N] or, for
     b_nk configurations, [chains, blocks, N, K]; b_logical is always the
-    [chains, blocks, K, N] view used by the reference.
+    [chains, blocks, K, N] view used by the reference. operands="dense"
+    (FP8 only) draws every A and B entry from {+-0.5, +-1, +-2} instead of
+    the reference's one-hot A: each dot entry is a multiple of 1/4 of
+    magnitude at most 4*K, so 1024 accumulations stay exact in fp32 for K <= 2048.
     """
     torch = _torch()
     m, n, k, chains = config["tile_m"], config["tile_n"], config["tile_k"], config["chains"]
     generator = _generator(device, seed)
     store = storage_dtype(dtype)
-    if dtype == "fp8":
+    if operands not in ("lattice", "dense") or (operands == "dense" and dtype != "fp8"):
+        raise ValueError(f"operand set {operands!r} is not defined for {dtype}")
+    if operands == "dense":
+        palette = torch.tensor(FP8_DENSE_SET, device=device)
+        a = palette[torch.randint(len(FP8_DENSE_SET), (blocks, m, k), device=device, generator=generator)].to(store)
+        b = palette[torch.randint(len(FP8_DENSE_SET), (chains, blocks, k, n), device=device,
+                                  generator=generator)].to(store)
+    elif dtype == "fp8":
         # One-hot rows of 1/16 in A and signs/16 in B: every dot is +-1/256.
         a = torch.zeros((blocks, m, k), device=device)
         hot = torch.randint(k, (blocks, m, 1), device=device, generator=generator)
@@ -202,6 +215,24 @@ def _smallest(configs):
     return min(configs, key=lambda config: config["tile_m"] * config["tile_n"] * config["tile_k"])
 
 
+def fp32_probe_matrix(size: int = 32):
+    """A of the FP32 probe: 1+2^-12 everywhere (lost by TF32, BF16 and FP16 rounding), 1+2^-9 at
+    [0, 1] (lost by BF16) and 2^20 at [0, 2] (beyond FP16's range) (bench_tensor.py:678-687)."""
+    torch = _torch()
+    probe = torch.full((size, size), 1.0 + 2.0**-12, dtype=torch.float32)
+    probe[0, 1], probe[0, 2] = 1.0 + 2.0**-9, 2.0**20
+    return probe
+
+
+def fp64_probe_matrix(size: int = 32, inner: int = 16):
+    """A of the FP64 probe: 1+2^-40 (lost by any FP32 rounding) with row r's column 0 set to r+1,
+    so a permuted output row is visible (bench_tensor.py:728-735)."""
+    torch = _torch()
+    probe = torch.full((size, inner), 1.0 + 2.0**-40, dtype=torch.float64)
+    probe[:, 0] = torch.arange(1, size + 1, dtype=torch.float64)
+    return probe
+
+
 def validate_fp32_precision(device, configs) -> dict:
     """IEEE vs TF32/BF16/FP16 probe through the peak kernel (bench_tensor.py:675-714).
 
@@ -212,8 +243,7 @@ def validate_fp32_precision(device, configs) -> dict:
     config = _smallest([c for c in configs if not c["b_nk"]])
     m, n, k = config["tile_m"], config["tile_n"], config["tile_k"]
     size = 32
-    probe = torch.full((size, size), 1.0 + 2.0**-12, dtype=torch.float32)
-    probe[0, 1], probe[0, 2] = 1.0 + 2.0**-9, 2.0**20
+    probe = fp32_probe_matrix(size)
     a = torch.zeros((1, m, k), dtype=torch.float32)
     a[0, :size, :size] = probe
     b = torch.zeros((config["chains"], 1, k, n), dtype=torch.float32)
@@ -240,8 +270,7 @@ def validate_fp64_precision(device, configs) -> dict:
     m, n, k = config["tile_m"], config["tile_n"], config["tile_k"]
     size, inner = 32, 16
     a = torch.zeros((1, m, k), dtype=torch.float64)
-    a[0, :size, :inner] = 1.0 + 2.0**-40
-    a[0, :size, 0] = torch.arange(1, size + 1, dtype=torch.float64)
+    a[0, :size, :inner] = fp64_probe_matrix(size, inner)
     b = torch.zeros((config["chains"], 1, k, n), dtype=torch.float64)
     b[:, 0, :inner, :size] = torch.eye(inner, size, dtype=torch.float64)
     c = torch.empty((config["chains"], 1, m, n), dtype=torch.float64, device=device)

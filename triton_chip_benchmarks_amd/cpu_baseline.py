@@ -97,6 +97,38 @@ def matmul_baseline(dtype: str, size: int, budget_s: float = 2.0) -> dict:
                    f"{size}x{size}x{size}", repeats)
 
 
+def gemm_sample_baseline(dtype: str, rows: int, n: int, k: int, budget_s: float = 2.0) -> dict:
+    """torch.matmul on the host of a [rows, K] slice of A against the whole [K, N] B.
+
+    The same K and N as the device GEMM with fewer rows of A: float32
+    (float64 for fp64), the reference's check arithmetic with the narrow
+    formats upcast (bench_tensor.py:277-286).
+    """
+    torch = _torch()
+    compute = torch.float64 if dtype == "fp64" else torch.float32
+    a = torch.randn((rows, k), dtype=compute)
+    b = torch.randn((k, n), dtype=compute)
+    seconds, repeats = best_seconds(lambda: torch.matmul(a, b), budget_s)
+    unit = "TOPS" if dtype == "int8" else "TFLOP/s"
+    upcast = "" if dtype in ("fp32", "fp64") else f", {dtype} operands upcast"
+    return _result(2 * rows * n * k / (seconds * 1e12), unit,
+                   f"torch.matmul on the host in {str(compute)[6:]}{upcast}", f"{rows}x{n}x{k} (rows of A sampled)",
+                   repeats)
+
+
+def tile_batch_baseline(dtype: str, blocks: int, m: int, n: int, k: int, budget_s: float = 2.0) -> dict:
+    """Batched torch.matmul on the host of `blocks` resident tiles [M, K] x [K, N] (one iteration, one chain)."""
+    torch = _torch()
+    compute = torch.float64 if dtype == "fp64" else torch.float32
+    a = torch.randn((blocks, m, k), dtype=compute)
+    b = torch.randn((blocks, k, n), dtype=compute)
+    seconds, repeats = best_seconds(lambda: torch.matmul(a, b), budget_s)
+    unit = "TOPS" if dtype == "int8" else "TFLOP/s"
+    return _result(2 * blocks * m * n * k / (seconds * 1e12), unit,
+                   f"batched torch.matmul on the host in {str(compute)[6:]}", f"{blocks} tiles of {m}x{n}x{k}",
+                   repeats)
+
+
 def _dp4a_step(x, weights, bias):
     """x <- sum_j byte_j(x) * w_j + b on int32 lanes (signed bytes, wrapping int32)."""
     total = bias.clone()
