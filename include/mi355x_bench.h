@@ -171,16 +171,30 @@ const char* mb_gemm_kernel_name(int format, const mb_gemm_config* config);
 /* C = A . B with A row-major [m][k] and B column-major, i.e. stored [n][k]
  * (both K-contiguous); C row-major [m][n] in the format's accumulator type
  * (fp32; int32 for I8; fp64 for F64). MXFP4: A and B hold two E2M1 codes per
- * byte along K (even k in the low nibble), scale_a [m][k/32] and scale_b
- * [n][k/32] are E8M0. K * element bits must be a multiple of 128 (16-byte
+ * byte along K (even k in the low nibble); scale_a and scale_b are E8M0 in
+ * K-step blocks, [ceil(k/256)][m][8] and [ceil(k/256)][n][8] bytes, where
+ * [b][r][g] scales row r over K elements 256b+32g .. 256b+32g+31 (entries
+ * past K are ignored): one 256-element K step of a tile reads one contiguous
+ * run of 8 bytes per row. K * element bits must be a multiple of 128 (16-byte
  * rows); other shapes are bounded by a checked kernel variant. group_m = 0
  * selects the default band of 8 tile rows.
  * Replaces: bench_tensor.py:172-209 (_gemm_kernel) and 235-246 (_launch),
- * whose B is row-major [k][n]. */
+ * whose B is row-major [k][n]; the reference has no MXFP4 GEMM (FP4 is refused
+ * in its GEMM mode, bench_tensor.py:1404-1407), so the scale layout is this
+ * library's. */
 int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_bytes, const void* b,
             uint64_t b_bytes, const void* scale_a, uint64_t scale_a_bytes, const void* scale_b,
             uint64_t scale_b_bytes, void* c, uint64_t c_bytes, uint32_t m, uint32_t n, uint32_t k,
             uint32_t group_m, void* stream);
+
+/* Registered name of the kernel mb_gemm launches for this call (the tile's
+ * fast kernel, or its "_checked" variant for shapes the fast kernel does not
+ * take), for the instruction and resource audit of what actually runs; NULL
+ * with mb_last_error() set for an invalid call.
+ * Replaces: the CompiledKernel the reference's launch returns for its audit
+ * (bench_tensor.py:594-600, 988). */
+const char* mb_gemm_launched_kernel(int format, const mb_gemm_config* config, uint32_t m, uint32_t n, uint32_t k,
+                                    const void* scale_a, const void* scale_b);
 
 /* ---- vector: register-resident arithmetic chains ------------------------ */
 

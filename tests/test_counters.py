@@ -1,0 +1,108 @@
+"""CPU tests of the counter recipe's summary (triton_chip_benchmarks_amd.counters).
+
+A synthetic rocprofv3 counter CSV with known values checks each derived
+figure against its formula worked by hand: clock, MFMA busy, VALU issue
+utilisation, wave waits, L2 hit rate, and HBM bytes calibrated against the
+1 GiB copy; plus the demangled-name mapping and attaching summaries to rows.
+"""
+
+import csv
+import json
+
+import pytest
+
+from triton_chip_benchmarks_amd import counters
+
+COPY = ("void mb::(anonymous namespace)::copy_kernel<unsigned int __vector(4), 1, 2>"
+        "(unsigned int __vector(4) const*, unsigned int __vector(4)*, unsigned long)")
+GEMM = ("void mb::(anonymous namespace)::gemm_dma_kernel<mb::MfmaBf16, 128, 2, 4>(unsigned char const*, "
+        "unsigned char const*, unsigned char const*, unsigned char const*, mb::MfmaBf16::Out*, int, int, int, int)")
+FIELDS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
+          "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+          "Accum_VGPR_Count", "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+
+def _write_pass(directory, records):
+    directory.mkdir(parents=True)
+    with (directory / "run_counter_collection.csv").open("w", newline="") as stream:
+        writer = csv.DictWriter(stream, FIELDS)
+        writer.writeheader()
+        for dispatch, kernel, counter, value, duration_ns in records:
+            row = dict.fromkeys(FIELDS, 0)
+            row.update(Dispatch_Id=dispatch, Kernel_Name=kernel, Counter_Name=counter, Counter_Value=value,
+                       Start_Timestamp=1000, End_Timestamp=1000 + duration_ns)
+            writer.writerow(row)
+
+
+def test_registered_names_of_demangled_kernels():
+    assert counters.registered_name(COPY) == "copy_dwordx4_vpt1_stream"
+    assert counters.registered_name(GEMM) == "gemm_bf16_256x256x64"
+    assert counters.registered_name(
+        "void mb::(anonymous namespace)::tensor_peak_kernel<mb::MfmaMxfp4, 128, 128, 256, 2, 2, 2, false>"
+        "(unsigned char const*)") == "tensor_peak_mxfp4_128x128x256_c2_kn"
+    assert counters.registered_name(
+        "void mb::(anonymous namespace)::gemm_kernel<mb::MfmaF64, 64, 64, 16, 2, 2, true>(int)") == \
+        "gemm_f64_64x64x16_checked"
+    assert counters.registered_name("void mb::(anonymous namespace)::vector_dot4_kernel<16>(int const*)") == \
+        "vector_dot4_u16"
+    assert counters.registered_name("Cijk_Alik_Bljk_BBS_BH(int)") == "Cijk_Alik_Bljk_BBS_BH"
+
+
+def test_summary_formulas_and_copy_calibration(tmp_path):
+    cycles_per_xcd, duration = 2_000_000, 1_000_000  # 2e6 cycles in 1 ms: 2 GHz
+    grbm = cycles_per_xcd * counters.XCDS
+    simd_cycles = cycles_per_xcd * counters.SIMDS
+    _write_pass(tmp_path / "sq", [
+        (1, GEMM, "GRBM_GUI_ACTIVE", grbm, duration),
+        (1, GEMM, "SQ_VALU_MFMA_BUSY_CYCLES", 0.75 * simd_cycles, duration),
+        (1, GEMM, "SQ_INSTS_VALU", 0.05 * simd_cycles / 4, duration),
+        (1, GEMM, "SQ_WAVE_CYCLES", 1000, duration), (1, GEMM, "SQ_WAIT_ANY", 250, duration),
+        (1, GEMM, "SQ_INSTS_LDS", 10, duration), (1, GEMM, "SQ_LDS_BANK_CONFLICT", 0, duration),
+        (1, GEMM, "SQ_BUSY_CYCLES", 1, duration)])
+    _write_pass(tmp_path / "l2", [
+        (1, GEMM, "GRBM_GUI_ACTIVE", grbm, duration), (1, GEMM, "TCP_TCC_READ_REQ_sum", 100, duration),
+        (1, GEMM, "TCC_HIT_sum", 80, duration), (1, GEMM, "TCC_MISS_sum", 20, duration),
+        (1, GEMM, "TCC_REQ_sum", 100, duration)])
+    # The copy reads 2^30 bytes and FETCH_SIZE reports half of them; WRITE_SIZE reports them all.
+    _write_pass(tmp_path / "fetch", [(2, COPY, "FETCH_SIZE", 2**19, 300_000),
+                                     (3, GEMM, "FETCH_SIZE", 2**18, duration)])
+    _write_pass(tmp_path / "write", [(2, COPY, "WRITE_SIZE", 2**20, 300_000),
+                                     (3, GEMM, "WRITE_SIZE", 2**16, duration)])
+    summary = counters.summarize(tmp_path)
+    assert summary["calibration_kernel"] == "copy_dwordx4_vpt1_stream"
+    assert summary["fetch_size_bytes_per_byte"] == pytest.approx(0.5)
+    assert summary["write_size_bytes_per_byte"] == pytest.approx(1.0)
+    gemm = summary["kernels"]["gemm_bf16_256x256x64"]
+    assert gemm["clock_ghz"] == pytest.approx(2.0)
+    assert gemm["mfma_busy"] == pytest.approx(0.75)
+    assert gemm["valu_issue_util"] == pytest.approx(0.05)
+    assert gemm["wave_wait_frac"] == pytest.approx(0.25)
+    assert gemm["l2_hit_rate"] == pytest.approx(0.8)
+    assert gemm["mfma_busy_times_clock_over_peak_clock"] == pytest.approx(0.75 * 2.0 / 2.4)
+    assert gemm["hbm_read_bytes"] == pytest.approx(2**18 * 1024 / 0.5)
+    assert gemm["hbm_write_bytes"] == pytest.approx(2**16 * 1024)
+    copy = summary["kernels"]["copy_dwordx4_vpt1_stream"]
+    assert copy["hbm_read_bytes"] == pytest.approx(2**30) and copy["hbm_write_bytes"] == pytest.approx(2**30)
+    assert "| `gemm_bf16_256x256x64` |" in counters.markdown(summary)
+
+    report = {"results": [{"metric": "tensor_bf16", "kernel": "gemm_bf16_256x256x64"},
+                          {"metric": "memory_bandwidth", "kernel": "copy_x",
+                           "patterns": {"copy": {"kernel": "copy_dwordx4_vpt1_stream"}}},
+                          {"metric": "tensor_tf32", "kernel": None}]}
+    assert counters.attach(report, json.loads(json.dumps(summary))) == 1
+    assert report["results"][0]["counters"]["mfma_busy"] == pytest.approx(0.75)
+    assert report["results"][1]["patterns"]["copy"]["counters"]["hbm_read_bytes"] == pytest.approx(2**30)
+    assert "counters" not in report["results"][2]
+
+
+def test_every_pass_fits_one_rocprofv3_run():
+    limits = {"SQ_": 8, "GRBM_": 2, "TCP_": 4}
+    for name, group in counters.PASSES.items():
+        for prefix, limit in limits.items():
+            assert sum(c.startswith(prefix) for c in group) <= limit, name
+        tcc = sum(c.startswith("TCC_") for c in group) + 3 * group.count("FETCH_SIZE") + 2 * group.count(
+            "WRITE_SIZE")
+        assert tcc <= 4, name
+    command = counters.rocprof_command(["SQ_WAVE_CYCLES"], "/tmp/x", ["python3", "prog.py"])
+    assert command[command.index("--") + 1:] == ["python3", "prog.py"]
+    assert not {"--sys-trace", "-s", "--runtime-trace", "-r"} & set(command)

@@ -173,3 +173,22 @@ def test_fp64_probe_detects_fp32_fallback_and_row_permutation():
     assert not np.array_equal(permuted, exact)
     assert sorted(map(tuple, permuted.tolist())) == sorted(map(tuple, exact.tolist()))
     assert np.array_equal(bench_tensor.fp64_probe_matrix().numpy(), a)
+
+
+def test_mx_scale_blocks_layout():
+    """formats.mx_scale_blocks: [rows][K/32] -> [ceil(K/256)][rows][8], block b row r group g = scale of
+    row r for K elements 256b+32g.., padding 127; checked entry by entry on a ragged K."""
+    from triton_chip_benchmarks_amd import formats
+
+    rows, groups = 5, 19  # K = 608: three blocks, the last holding 3 groups
+    scales = torch.arange(rows * groups, dtype=torch.uint8).view(rows, groups)
+    blocks = formats.mx_scale_blocks(scales)
+    assert blocks.shape == (3, rows, 8) and blocks.is_contiguous()
+    for b in range(3):
+        for r in range(rows):
+            for g in range(8):
+                expected = int(scales[r, 8 * b + g]) if 8 * b + g < groups else 127
+                assert int(blocks[b, r, g]) == expected
+    # One K step (block b) of rows r0..r0+n-1 is one contiguous run of 8*n bytes.
+    flat = blocks.reshape(-1)
+    assert flat[(1 * rows + 2) * 8:(1 * rows + 4) * 8].tolist() == blocks[1, 2:4].reshape(-1).tolist()

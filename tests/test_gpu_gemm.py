@@ -46,6 +46,16 @@ def _operand_values(rng, dtype, rows, k, normal=False):
     return ot.ternary_lattice(rng, (rows, k))
 
 
+def _scale_blocks(scales):
+    """[rows][K/32] E8M0 codes -> mb_gemm's K-step blocks [ceil(K/256)][rows][8] (padding 127)."""
+    rows, groups = scales.shape
+    out = np.full((-(-groups // 8), rows, 8), 127, dtype=np.uint8)
+    for block in range(out.shape[0]):
+        part = scales[:, 8 * block:8 * block + 8]
+        out[block, :, :part.shape[1]] = part
+    return out
+
+
 def _device_operand(torch, values, dtype):
     values = np.ascontiguousarray(values)
     if dtype == "bf16":
@@ -75,8 +85,8 @@ def _run_gemm(dtype, config, m, n, k, rng, normal=False, keep_device=False):
         codes_b = rng.integers(0, 16, (n, k), dtype=np.uint8)
         a = torch.from_numpy(ot.pack_e2m1(codes_a)).cuda()
         b = torch.from_numpy(ot.pack_e2m1(codes_b)).cuda()
-        scales = (torch.full((m, k // 32), 127, dtype=torch.uint8, device="cuda"),
-                  torch.full((n, k // 32), 127, dtype=torch.uint8, device="cuda"))
+        scales = (torch.full((-(-k // 256), m, 8), 127, dtype=torch.uint8, device="cuda"),
+                  torch.full((-(-k // 256), n, 8), 127, dtype=torch.uint8, device="cuda"))
         a_values, b_values = ot.e2m1_decode(codes_a), ot.e2m1_decode(codes_b)
     else:
         a_values = _operand_values(rng, dtype, m, k, normal or dtype == "fp64")
@@ -170,7 +180,9 @@ def test_mxfp4_gemm_applies_each_rows_group_scale(gpu):
     """E8M0 scales drawn from {126, 127, 128} per (row, 32-element group): a
     wrong row or group index, or a scale applied to the wrong operand, moves
     the result off the exact oracle. Products are multiples of 2^-4 below 145
-    and K <= 1024, so every partial sum is exact in fp32 in any order."""
+    and K <= 4096, so every partial sum is exact in fp32 in any order. The
+    scales are passed in mb_gemm's K-step block layout; shapes cover the fast
+    path (>= 4 even K steps) and the checked one (2 steps, ragged M/N/K)."""
     import torch
 
     from triton_chip_benchmarks_amd import _native
@@ -179,6 +191,7 @@ def test_mxfp4_gemm_applies_each_rows_group_scale(gpu):
     for config in _configs("fp4"):
         shapes = [(config["tile_m"], config["tile_n"], 2 * config["tile_k"]),
                   (2 * config["tile_m"], config["tile_n"], 4 * config["tile_k"]),
+                  (config["tile_m"], 2 * config["tile_n"], 2048),
                   (config["tile_m"] + 37, config["tile_n"] - 5, 160)]
         for m, n, k in shapes:
             print(f"gemm fp4 scaled tile {config['tile_m']}x{config['tile_n']}x{config['tile_k']} shape {m}x{n}x{k}",
@@ -190,7 +203,7 @@ def test_mxfp4_gemm_applies_each_rows_group_scale(gpu):
             c = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
             _native.gemm("fp4", config, torch.from_numpy(ot.pack_e2m1(codes_a)).cuda(),
                          torch.from_numpy(ot.pack_e2m1(codes_b)).cuda(), c, m, n, k,
-                         torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda())
+                         torch.from_numpy(_scale_blocks(sa)).cuda(), torch.from_numpy(_scale_blocks(sb)).cuda())
             torch.cuda.synchronize()
             a_values = ot.e2m1_decode(codes_a) * np.repeat(ot.e8m0_decode(sa), 32, axis=1)
             b_values = ot.e2m1_decode(codes_b) * np.repeat(ot.e8m0_decode(sb), 32, axis=1)

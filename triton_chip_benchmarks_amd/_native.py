@@ -101,6 +101,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                               _ptr, _u64, _u32, _u32, _ptr]),
     "mb_gemm_configs": (_i32, [_i32, ctypes.POINTER(GemmConfig), _i32]),
     "mb_gemm_kernel_name": (ctypes.c_char_p, [_i32, ctypes.POINTER(GemmConfig)]),
+    "mb_gemm_launched_kernel": (ctypes.c_char_p, [_i32, ctypes.POINTER(GemmConfig), _u32, _u32, _u32, _ptr, _ptr]),
     "mb_gemm": (_i32, [_i32, ctypes.POINTER(GemmConfig), _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64, _ptr, _u64,
                        _u32, _u32, _u32, _u32, _ptr]),
     "mb_vector_kernel_name": (ctypes.c_char_p, [_i32, _u32]),
@@ -239,6 +240,15 @@ def _gemm_config(config: dict) -> GemmConfig:
 def gemm_kernel_name(dtype: str, config: dict) -> str | None:
     name = load().mb_gemm_kernel_name(MATRIX_FORMATS[dtype], ctypes.byref(_gemm_config(config)))
     return name.decode() if name else None
+
+
+def gemm_launched_kernel(dtype: str, config: dict, m: int, n: int, k: int, scale_a=None, scale_b=None) -> str:
+    """Registered name of the kernel mb_gemm launches for this shape (fast or checked path)."""
+    name = load().mb_gemm_launched_kernel(MATRIX_FORMATS[dtype], ctypes.byref(_gemm_config(config)), m, n, k,
+                                          _buffer(scale_a)[0], _buffer(scale_b)[0])
+    if not name:
+        raise NativeError(last_error())
+    return name.decode()
 
 
 def gemm(dtype: str, config: dict, a, b, c, m: int, n: int, k: int, scale_a=None, scale_b=None, group_m: int = 0,

@@ -4,31 +4,40 @@
 // C[M][N] = A[M][K] . B[K][N] with A row-major and B column-major, so both
 // operands are K-contiguous in memory ("NT"); the accumulator type is the
 // instruction's (fp32, int32 for INT8, fp64 for FP64). MXFP4 operands carry
-// one E8M0 scale per 32 K elements: SA[M][K/32], SB[N][K/32].
+// one E8M0 scale per 32 K elements in K-step blocks: SA[ceil(K/256)][M][8],
+// SB[ceil(K/256)][N][8], where [b][r][g] scales row r over K elements
+// 256b + 32g .. 256b + 32g + 31, so the scales of one 256-element K step of a
+// tile are one contiguous run of 8 bytes per row.
 // Replaces the reference's _gemm_kernel (bench_tensor.py:172-209), whose B is
 // row-major; the MI355X kernel takes K-contiguous B (layout prepared outside
 // timing by the caller).
 //
-// Design:
-//   * a workgroup of WAVES_M x WAVES_N waves owns a BM x BN tile; each wave a
-//     (BM/WAVES_M) x (BN/WAVES_N) block of 32x32 (16x16 for FP64) MFMA tiles;
-//   * each K step stages BM x BK and BN x BK operand tiles from HBM into a
-//     padded, double-buffered LDS tile with 16-byte coalesced loads; the loads
-//     of step k+1 are in flight while the MFMAs of step k run, and one barrier
-//     per step separates the buffers;
-//   * workgroups are numbered XCD-first: the hardware deals consecutive
-//     workgroup ids round-robin over the 8 XCDs, so id i is remapped to the
-//     i/8-th tile of XCD i%8's contiguous share, and within that share tiles
-//     are walked in GROUP_M-row bands, keeping A and B panels hot in the XCD's L2;
-//   * CHECKED instantiations bound every load and store for ragged shapes.
-//
-// 256x256 tiles of the 8- and 16-bit formats use gemm_dma_kernel instead when
-// the shape divides the tile: 8 waves (2 per SIMD), operands fed straight from
-// L2 into LDS by buffer_load_dwordx4 ... lds (no VGPR staging, no ds_write),
-// XOR-swizzled LDS rows (conflict-free ds_read_b128 without padding), and
-// fragment reads of substep s+1 issued ahead of the MFMAs of substep s.
+// Three kernels:
+//   * gemm_staged_kernel: 256x256 tiles of the 16-byte-fragment formats (BF16,
+//     FP16, INT8, MXFP4) when the shape divides the tile. Four waves, one per
+//     SIMD, each owning 128x128 outputs (16 accumulators of 32x32 in AGPRs).
+//     Operands flow global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128
+//     bytes of every row) is loaded two steps ahead into one of two register
+//     sets, written to one of two LDS stages a step ahead, and read back as
+//     fragments one substep ahead. Loads, stage writes and fragment reads are
+//     spread across the step's MFMAs, so no burst of memory instructions
+//     stalls the in-order MFMA issue; one barrier per step.
+//   * gemm_dma_kernel: 256x256 FP8 tiles, operands fed straight from L2 into
+//     LDS by buffer_load_dwordx4 ... lds (8 waves, 2 per SIMD), faster for the
+//     32-byte FP8 fragments, whose double buffer does not fit beside the
+//     staged kernel's registers.
+//   * gemm_kernel: every other tile and every ragged shape (CHECKED
+//     instantiations bound each load and store), operands staged through a
+//     padded, double-buffered LDS tile with 16-byte loads.
+// All three number workgroups XCD-first: the hardware deals consecutive ids
+// round-robin over the 8 XCDs, so id i is remapped to the i/8-th tile of XCD
+// i%8's contiguous share, walked in GROUP_M-row bands that keep A and B panels
+// hot in that XCD's L2.
 #include "mb_internal.h"
 #include "mb_mfma.h"
+
+#include <cstring>
+#include <type_traits>
 
 namespace mb {
 namespace {
@@ -127,6 +136,10 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
   const int lrow = lane % Op::M, lgroup = lane / Op::M;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES;
   const int scale_cols = Op::SCALED ? K / 32 : 0;
+  // Block layout: group col of row r at ((col / 8) * rows + r) * 8 + col % 8.
+  auto scale_at = [](const uint8_t* S, int rows, int r, int col) {
+    return static_cast<int>(S[(static_cast<int64_t>(col >> 3) * rows + r) * 8 + (col & 7)]);
+  };
 
   typename Op::Acc acc[T::TM][T::TN];
 #pragma unroll
@@ -154,8 +167,7 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
         for (int ks = 0; ks < T::KSTEPS; ++ks) {
           const int row = m0 + wm * T::WM + tm * Op::M + lrow;
           const int col = kt * T::GROUPS + ks * MfmaGeometry<Op>::LANE_GROUPS + lgroup;
-          sa[tm][ks] = (!CHECKED || (row < M && col < scale_cols)) ? SA[static_cast<int64_t>(row) * scale_cols + col]
-                                                                    : 127;
+          sa[tm][ks] = (!CHECKED || (row < M && col < scale_cols)) ? scale_at(SA, M, row, col) : 127;
         }
 #pragma unroll
       for (int tn = 0; tn < T::TN; ++tn)
@@ -163,9 +175,7 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
         for (int ks = 0; ks < T::KSTEPS; ++ks) {
           const int col_n = n0 + wn * T::WN + tn * Op::N + lrow;
           const int col = kt * T::GROUPS + ks * MfmaGeometry<Op>::LANE_GROUPS + lgroup;
-          sb[tn][ks] = (!CHECKED || (col_n < N && col < scale_cols))
-                           ? SB[static_cast<int64_t>(col_n) * scale_cols + col]
-                           : 127;
+          sb[tn][ks] = (!CHECKED || (col_n < N && col < scale_cols)) ? scale_at(SB, N, col_n, col) : 127;
         }
     } else {
 #pragma unroll
@@ -208,20 +218,15 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
       }
 }
 
-// ---- DMA-fed 256x256 kernel ------------------------------------------------
+// ---- shared pieces of the 256x256 kernels ---------------------------------
 
 // One 16-byte-per-lane LDS DMA: lane l's 16 bytes land at lds_addr + 16 * l.
 // Issued as inline assembly so the compiler's wait-count pass does not force a
-// full vmcnt(0) before every LDS read; the kernel waits explicitly instead.
+// full vmcnt(0) before every LDS read; the kernels wait explicitly instead, or
+// (staged kernel) issue it ahead of compiler-visible loads whose in-order
+// vmcnt waits then cover it.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, uint32_t lds_addr) {
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
-               "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory");
-}
-
-// One 4-byte-per-lane LDS DMA (E8M0 scale rows): lane l's 4 bytes land at lds_addr + 4 * l.
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, uint32_t lds_addr) {
-  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
                "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory");
 }
@@ -231,16 +236,41 @@ __device__ __forceinline__ void wait_all_dma() { asm volatile("s_waitcnt vmcnt(0
 // Word 3 of a gfx9 buffer resource: 32-bit data format, no swizzle, raw offsets.
 constexpr int kBufferWord3 = 0x00020000;
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const uint8_t* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, bytes, kBufferWord3);
+}
+
+// Tile (tile_m, tile_n) of workgroup blockIdx.x: XCD-first numbering, then
+// GROUP_M-row bands (see the file comment).
+__device__ __forceinline__ void band_tile(int tiles_m, int tiles_n, int group_m, int& tile_m, int& tile_n) {
+  const int count = gridDim.x;
+  int pid = blockIdx.x;
+  if (count % kXcds == 0) pid = (pid % kXcds) * (count / kXcds) + pid / kXcds;
+  const int band = group_m * tiles_n;
+  const int first_m = (pid / band) * group_m;
+  const int rows_in_band = min(tiles_m - first_m, group_m);
+  tile_m = first_m + (pid % band) % rows_in_band;
+  tile_n = (pid % band) / rows_in_band;
+}
+
+// Barrier that orders LDS only: global loads in flight stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---- DMA-fed 256x256 kernel (FP8) ------------------------------------------
+
 // C = A . B^T for M, N multiples of 256 and K * bits multiples of ROWB * 8;
 // A, B byte offsets must fit in 31 bits. Each K step stages a 256 x ROWB-byte
-// slice of A and of B (one LDS stage, double-buffered); for MXFP4 the stage
-// also holds the step's E8M0 scales, 256 rows x ROWB/16 bytes for A and for B. LDS row r holds its
+// slice of A and of B (one LDS stage, double-buffered). LDS row r holds its
 // 16-byte chunk c at position c ^ ((r / (256 / ROWB)) % (ROWB / 16)): any 16
 // consecutive rows read at one logical chunk hit 16 distinct bank groups.
 template <class Op, int ROWB, int WAVES_M, int WAVES_N>
 __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
-    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__ SA,
-                    const uint8_t* __restrict__ SB, typename Op::Out* __restrict__ C, int M, int N, int K,
+    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
+                    const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
                     int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 256, BN = 256;
@@ -248,41 +278,28 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
   constexpr int CPR = ROWB / 16;      // 16-byte chunks per LDS row
   constexpr int RPI = 1024 / ROWB;    // rows one DMA instruction fills (64 lanes x 16 bytes)
   constexpr int RPB = 256 / ROWB;     // rows per 256 bytes: the swizzle period
-  constexpr int DATA = (BM + BN) * ROWB;
-  // MXFP4: ROWB bytes hold 2*ROWB E2M1 codes, i.e. ROWB/16 scale bytes per row.
-  constexpr int SCALE_ROW = Op::SCALED ? ROWB / 16 : 0;
-  constexpr int STAGE = DATA + (BM + BN) * SCALE_ROW;
+  constexpr int STAGE = (BM + BN) * ROWB;
   constexpr int INSTR = (BM + BN) / RPI / NW;  // DMA instructions per wave per K step
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / Op::M, TN = WN / Op::N;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES, KSTEPS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
+  static_assert(!Op::SCALED, "scaled formats use the staged kernel");
   static_assert((BM / RPI) % NW == 0, "an instruction's rows are all A or all B, whatever the wave");
   static_assert(ROWB % KB == 0 && Op::LANE_BYTES % 16 == 0 && Op::M == 32, "whole 32x32 instructions per step");
-  static_assert(!Op::SCALED || (SCALE_ROW == 8 && (BM + BN) * SCALE_ROW / 256 == 2 * NW),
-                "scale DMA: one 4-byte-lane instruction of A rows and one of B rows per wave");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
   // The array is otherwise written only by DMA, which the optimizer does not
   // see as a store; one plain (never executed) store keeps its reads live.
   if (K < 0) lds[threadIdx.x] = 0;
 
-  const int tiles_m = M / BM, tiles_n = N / BN;
-  const int count = gridDim.x;
-  int pid = blockIdx.x;
-  if (count % kXcds == 0) pid = (pid % kXcds) * (count / kXcds) + pid / kXcds;
-  const int band = group_m * tiles_n;
-  const int first_m = (pid / band) * group_m;
-  const int rows_in_band = min(tiles_m - first_m, group_m);
-  const int tile_m = first_m + (pid % band) % rows_in_band;
-  const int tile_n = (pid % band) / rows_in_band;
+  int tile_m, tile_n;
+  band_tile(M / BM, N / BN, group_m, tile_m, tile_n);
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int row_bytes = K * Op::ELEM_BITS / 8;
   const int k_steps = row_bytes / ROWB;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // Each resource covers exactly this tile's 256 rows of its operand.
-  const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(A + static_cast<int64_t>(m0) * row_bytes), (short)0, BM * row_bytes, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(B + static_cast<int64_t>(n0) * row_bytes), (short)0, BN * row_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_a = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
+  const __amdgpu_buffer_rsrc_t rsrc_b = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BN * row_bytes);
   const uint32_t lds_base =
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds)));
   // DMA instruction j of this wave fills LDS rows rb*RPI .. rb*RPI+RPI-1 of the
@@ -295,18 +312,6 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
     const int chunk = (lane % CPR) ^ ((row / RPB) % CPR);
     voff[j] = (row < BM ? row : row - BM) * row_bytes + chunk * 16;
   }
-  // MXFP4 scales: wave w moves A scale rows 32w .. 32w+31 and the same B
-  // rows; lane l carries half l%2 of row 32w + l/2's SCALE_ROW bytes.
-  const int scale_cols = Op::SCALED ? K / 32 : 0;
-  __amdgpu_buffer_rsrc_t rsrc_sa = rsrc_a, rsrc_sb = rsrc_b;
-  int scale_voff = 0;
-  if constexpr (Op::SCALED) {
-    rsrc_sa = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SA + static_cast<int64_t>(m0) * scale_cols),
-                                                (short)0, BM * scale_cols, kBufferWord3);
-    rsrc_sb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SB + static_cast<int64_t>(n0) * scale_cols),
-                                                (short)0, BN * scale_cols, kBufferWord3);
-    scale_voff = (wave * 32 + lane / 2) * scale_cols + (lane % 2) * 4;
-  }
   auto issue = [&](int kt) {
     const uint32_t stage = lds_base + (kt & 1) * STAGE;
 #pragma unroll
@@ -314,10 +319,6 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
       const uint32_t dst = stage + (j * NW + wave) * 1024;
       if (j * NW < BM / RPI) dma16(rsrc_a, voff[j], kt * ROWB, dst);
       else dma16(rsrc_b, voff[j], kt * ROWB, dst);
-    }
-    if constexpr (Op::SCALED) {
-      dma4(rsrc_sa, scale_voff, kt * SCALE_ROW, stage + DATA + wave * 256);
-      dma4(rsrc_sb, scale_voff, kt * SCALE_ROW, stage + DATA + BM * SCALE_ROW + wave * 256);
     }
   };
 
@@ -355,20 +356,6 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
     __syncthreads();
     if (kt + 1 < k_steps) issue(kt + 1);
     const uint8_t* stage = lds + (kt & 1) * STAGE;
-    // MXFP4: a lane's scale for substep ks is group 2*ks + lgroup of its row;
-    // after shifting the row's 8 bytes by 8*lgroup, it is byte 2*ks, i.e. byte
-    // 0 of the value shifted by 16*ks (the instruction reads byte 0).
-    uint64_t srow_a[TM], srow_b[TN];
-    if constexpr (Op::SCALED) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        srow_a[i] = *reinterpret_cast<const uint64_t*>(stage + DATA + (wm * WM + i * 32 + lrow) * SCALE_ROW) >>
-                    (8 * lgroup);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        srow_b[j] = *reinterpret_cast<const uint64_t*>(stage + DATA + (BM + wn * WN + j * 32 + lrow) * SCALE_ROW) >>
-                    (8 * lgroup);
-    }
     typename Op::Frag fa[2][TM], fb[2][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa[0][i] = read(stage, wm * WM + i * 32 + lrow, 0);
@@ -388,14 +375,7 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          int scale_a = 0, scale_b = 0;
-          if constexpr (Op::SCALED) {
-            scale_a = static_cast<int>(srow_a[i] >> (16 * ks));
-            scale_b = static_cast<int>(srow_b[j] >> (16 * ks));
-          }
-          acc[i][j] = Op::mma(fa[cur][i], fb[cur][j], acc[i][j], scale_a, scale_b);
-        }
+        for (int j = 0; j < TN; ++j) acc[i][j] = Op::mma(fa[cur][i], fb[cur][j], acc[i][j], 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -408,6 +388,211 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
       for (int r = 0; r < Op::ACC_REGS; ++r) {
         const int row = m0 + wm * WM + i * 32 + Op::out_row(lane, r);
         const int col = n0 + wn * WN + j * 32 + lrow;
+        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+      }
+#endif
+}
+
+// ---- VGPR-staged 256x256 kernel (BF16, FP16, INT8, MXFP4) -------------------
+
+// C = A . B^T for M, N multiples of 256, K * bits a multiple of 1024 (128-byte
+// K steps) with an even number of at least 4 steps; A, B byte offsets and the
+// MXFP4 scale blocks must fit in 31 bits. Four waves in a 2x2 grid own 128x128
+// outputs each.
+//
+// LDS: regions [A stage 0][A stage 1][B stage 0][B stage 1] of 256 rows x 128
+// bytes (every stage and fragment offset is a ds_* immediate), then for MXFP4
+// a ring of four 4 KiB scale stages [256 A rows][256 B rows] x 8 bytes. Row r
+// of a region holds its 16-byte chunk c at r*128 + ((c ^ ((r >> 1) & 7)) << 4),
+// so the 16 rows a ds_read_b128 quarter-wave touches hit 16 bank groups.
+//
+// Per K step kt (stage s = kt & 1): the MFMAs of substep ks use fragments read
+// during substep ks-1 (the first from stage s during step kt-1's last
+// substep); register set V[kt & 1 ^ 1] holds step kt+1 (loaded at step kt-2),
+// which is written to stage s^1 over substeps 0..KS-2 and reloaded with step
+// kt+3 right behind each write; the barrier after substep KS-2 publishes
+// stage s^1 and ends every read of stage s^1's previous step. Past the last
+// step the loads repeat it and the extra writes and reads go unused, so all
+// steps run one branch-free body.
+template <class Op>
+__global__ void __launch_bounds__(256)
+    gemm_staged_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                       const uint8_t* __restrict__ SA, const uint8_t* __restrict__ SB,
+                       typename Op::Out* __restrict__ C, int M, int N, int K, int group_m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NL = 16;
+  constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB;
+  constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = Op::SCALED ? 4 : 0;
+  static_assert(Op::M == 32 && Op::LANE_BYTES == 16 && KS == 4, "16-byte 32x32 fragments, four substeps");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * REGION + SCALE_RING * SCALE_STAGE];
+  if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written (scale) reads live; never executed
+
+  int tile_m, tile_n;
+  band_tile(M / BM, N / BM, group_m, tile_m, tile_n);
+  const int m0 = tile_m * BM, n0 = tile_n * BM;
+  const int row_bytes = K * Op::ELEM_BITS / 8;
+  const int k_steps = row_bytes / ROWB, last = k_steps - 1;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BM * row_bytes);
+  // Load j of a step covers rows 32j .. 32j+31 of the A|B stage (j < 8: A);
+  // thread t moves row 32j + t/8, chunk t%8.
+  const int voff = (t >> 3) * row_bytes + (t & 7) * 16;
+  uint8_t* const wa = lds + (t >> 3) * ROWB + (((t & 7) ^ ((t >> 4) & 7)) << 4);
+  uint8_t* const wb = wa + 2 * REGION;
+  auto load = [&](i32x4 (&v)[NL], int kt, int j0, int j1) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = j0; j < j1; ++j)
+      v[j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           j < 8 ? ra : rb, voff, kt * ROWB + (j & 7) * 32 * row_bytes, 0));
+  };
+  auto store = [&](const i32x4 (&v)[NL], int s, int j0, int j1) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = j0; j < j1; ++j)
+      *reinterpret_cast<i32x4*>((j < 8 ? wa : wb) + s * REGION + (j & 7) * 32 * ROWB) = v[j];
+  };
+
+  // MXFP4 scales: wave w DMAs 1 KiB of a step's scale stage, rows 128(w&1) ..
+  // +127 of A (w < 2) or B, from block kt of SA or SB.
+  __amdgpu_buffer_rsrc_t rs = ra;
+  int s_rows = 0, s_row0 = 0;
+  uint32_t scale_lds = 0;
+  if constexpr (Op::SCALED) {
+    const int blocks = k_steps;  // 256 E2M1 elements per 128-byte step
+    rs = wave < 2 ? buffer_rsrc(SA, blocks * M * 8) : buffer_rsrc(SB, blocks * N * 8);
+    s_rows = wave < 2 ? M : N;
+    s_row0 = (wave < 2 ? m0 : n0) + (wave & 1) * 128;
+    scale_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                    (__attribute__((address_space(3))) uint8_t*)(lds + 4 * REGION))) + wave * 1024;
+  }
+  // Block `block` into ring slot (slot & 3); past the last step the block is
+  // clamped but the slot is not, so a slot still being read is never written.
+  auto scale_dma = [&](int slot, int block) __attribute__((always_inline)) {
+    if constexpr (Op::SCALED)
+      dma16(rs, lane * 16, (block * s_rows + s_row0) * 8, scale_lds + (slot & 3) * SCALE_STAGE);
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lrow = lane & 31, lgroup = lane >> 5;
+  // A lane's fragment of substep ks is its row's logical chunk 2ks + lgroup,
+  // i.e. the lane base XOR (ks << 5): only address bits 5..6 change, so
+  // region, stage and fragment offsets still add as immediates.
+  const int sw = ((lrow >> 1) & 7) ^ lgroup;
+  const uint32_t ra_off = (wm * 128 + lrow) * ROWB + (sw << 4);
+  const uint32_t rb_off = 2 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
+  using Frag8 = i32x4[8];
+  auto read = [&](Frag8& fr, int s, int ks) __attribute__((always_inline)) {
+    const uint32_t x = static_cast<uint32_t>(ks) << 5;
+    const uint8_t* pa = lds + (ra_off ^ x) + s * REGION;
+    const uint8_t* pb = lds + (rb_off ^ x) + s * REGION;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      fr[f] = *reinterpret_cast<const i32x4*>(pa + f * 32 * ROWB);
+      fr[4 + f] = *reinterpret_cast<const i32x4*>(pb + f * 32 * ROWB);
+    }
+  };
+  // MXFP4: one dword per fragment row holding the scales of its lane's four
+  // 32-element groups of a step (groups lgroup, 2+lgroup, 4+lgroup, 6+lgroup:
+  // substep ks uses byte ks), picked out of the row's 8 bytes by v_perm_b32.
+  const uint32_t pick = 0x06040200u + 0x01010101u * static_cast<uint32_t>(lgroup);
+  using Scales8 = uint32_t[8];
+  auto read_scales = [&](Scales8& sc, int kt) __attribute__((always_inline)) {
+    if constexpr (Op::SCALED) {
+      const uint8_t* st = lds + 4 * REGION + (kt & 3) * SCALE_STAGE;
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const int row = f < 4 ? wm * 128 + f * 32 + lrow : 256 + wn * 128 + (f - 4) * 32 + lrow;
+        const i32x2 r = *reinterpret_cast<const i32x2*>(st + row * 8);
+        sc[f] = __builtin_amdgcn_perm(static_cast<uint32_t>(r[1]), static_cast<uint32_t>(r[0]), pick);
+      }
+    }
+  };
+
+  typename Op::Acc acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = typename Op::Acc{};
+
+  i32x4 v0[NL], v1[NL];
+  Frag8 fa, fb;
+  Scales8 sa0, sa1;
+  // Prologue: steps 0 and 1 in flight, step 0 into stage 0, step 2 into v0.
+  // The wait for v0 before its stage write also covers the older scale DMAs.
+  scale_dma(0, 0);
+  scale_dma(1, min(1, last));
+  scale_dma(2, min(2, last));
+  load(v0, 0, 0, NL);
+  load(v1, 1, 0, NL);
+  store(v0, 0, 0, NL);
+  load(v0, 2, 0, NL);
+  lds_barrier();
+  read(fa, 0, 0);
+  read_scales(sa0, 0);
+
+  auto step = [&](int kt, int s, i32x4 (&vnext)[NL], Scales8& sc, Scales8& sc_next) __attribute__((always_inline)) {
+    auto substep = [&](auto ks_c) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ks_c)::value;
+      Frag8& cur = (ks & 1) ? fb : fa;
+      Frag8& nxt = (ks & 1) ? fa : fb;
+      if constexpr (ks + 1 < KS) {
+        read(nxt, s, ks + 1);
+      } else {
+        read(nxt, s ^ 1, 0);
+        read_scales(sc_next, kt + 1);
+      }
+      // This substep's share of step kt+1's stage writes (all before the
+      // barrier) and of step kt+3's loads, each behind the write that frees
+      // its registers; the scale DMA of step kt+3 goes first, so the in-order
+      // waits for these loads cover it.
+      constexpr int W0 = ks * NL / (KS - 1) < NL ? ks * NL / (KS - 1) : NL;
+      constexpr int W1 = (ks + 1) * NL / (KS - 1) < NL ? (ks + 1) * NL / (KS - 1) : NL;
+      constexpr int L0 = ks * NL / KS, L1 = (ks + 1) * NL / KS;
+      store(vnext, s ^ 1, W0, W1);
+      if constexpr (ks == 0) scale_dma(kt + 3, min(kt + 3, last));
+      load(vnext, min(kt + 3, last), L0, L1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (Op::SCALED)
+            acc[i][j] = Op::template mma_byte<ks>(cur[i], cur[4 + j], acc[i][j], sc[i], sc[4 + j]);
+          else
+            acc[i][j] = Op::mma(cur[i], cur[4 + j], acc[i][j], 0, 0);
+        }
+      // Interleave: after each MFMA, one of the next substep's fragment reads
+      // (front-loaded) and this substep's writes and loads, evenly spaced.
+      constexpr int WR = W1 - W0, LD = L1 - L0;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // MFMA
+        if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                         // DS read
+        if ((q + 1) * WR / 16 != q * WR / 16) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+        if ((q + 1) * LD / 16 != q * LD / 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      }
+      if constexpr (ks == KS - 2) lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    substep(std::integral_constant<int, 0>{});
+    substep(std::integral_constant<int, 1>{});
+    substep(std::integral_constant<int, 2>{});
+    substep(std::integral_constant<int, 3>{});
+  };
+  for (int kt = 0; kt < k_steps; kt += 2) {
+    step(kt, 0, v1, sa0, sa1);
+    step(kt + 1, 1, v0, sa1, sa0);
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < Op::ACC_REGS; ++r) {
+        const int row = m0 + wm * 128 + i * 32 + Op::out_row(lane, r);
+        const int col = n0 + wn * 128 + j * 32 + lrow;
         C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
       }
 #endif
@@ -435,9 +620,18 @@ void launch_gemm_dma(const uint8_t* a, const uint8_t* b, const uint8_t* sa, cons
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
-// launch: shapes that divide the tile (nullptr: none, use launch_checked);
-// launch_checked: any shape. dma_row_bytes > 0 marks a DMA kernel, whose K
-// step is that many bytes and whose operand offsets must fit in 31 bits.
+template <class Op>
+void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m,
+                        int n, int k, int group_m, hipStream_t stream) {
+  gemm_staged_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
+      a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+}
+
+// What a variant's fast launcher needs beyond a shape that divides its tile.
+enum GemmPath { kLdsPath = 0, kDmaPath = 1, kStagedPath = 2 };
+
+// launch: shapes that divide the tile and satisfy the path's rule (see
+// exact_shape); launch_checked: any shape.
 struct GemmVariant {
   int format;
   mb_gemm_config config;
@@ -447,7 +641,9 @@ struct GemmVariant {
   GemmLauncher launch_checked;
   int out_bytes;
   int elem_bits;
-  int dma_row_bytes;
+  int path;
+  const char* checked_name;
+  const void* checked_kernel;
 };
 
 #define MB_GEMM(FMT, OP, BM, BN, BK, WM, WN, NAME)                                                           \
@@ -459,11 +655,25 @@ struct GemmVariant {
               launch_gemm<OP, BM, BN, BK, WM, WN, true>,                                                     \
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
               OP::ELEM_BITS,                                                                                 \
-              0}
+              kLdsPath,                                                                                      \
+              NAME "_checked",                                                                               \
+              reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, true>)}
 
-// 256x256 tile: the DMA kernel (8 waves, 128-byte K steps) for exact shapes,
-// a checked LDS-staged kernel (tile CM x CN) for ragged ones.
-#define MB_GEMM_DMA(FMT, OP, BK, CM, CN, NAME)                                                               \
+// 256x256 tiles: the staged kernel (BK = 128 bytes of K) or, for FP8, the DMA
+// kernel for exact shapes; a checked LDS-staged kernel (tile CM x CN) for the rest.
+#define MB_GEMM_STAGED(FMT, OP, BK, CM, CN, NAME, CNAME)                                                          \
+  GemmVariant{FMT,                                                                                           \
+              mb_gemm_config{256, 256, BK, 256},                                                             \
+              NAME,                                                                                          \
+              reinterpret_cast<const void*>(gemm_staged_kernel<OP>),                                         \
+              launch_gemm_staged<OP>,                                                                        \
+              launch_gemm<OP, CM, CN, BK, 2, 2, true>,                                                       \
+              static_cast<int>(sizeof(typename OP::Out)),                                                    \
+              OP::ELEM_BITS,                                                                                 \
+              kStagedPath,                                                                                   \
+              CNAME,                                                                               \
+              reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>)}
+#define MB_GEMM_DMA(FMT, OP, BK, CM, CN, NAME, CNAME)                                                          \
   GemmVariant{FMT,                                                                                           \
               mb_gemm_config{256, 256, BK, 512},                                                             \
               NAME,                                                                                          \
@@ -472,22 +682,29 @@ struct GemmVariant {
               launch_gemm<OP, CM, CN, BK, 2, 2, true>,                                                       \
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
               OP::ELEM_BITS,                                                                                 \
-              128}
+              kDmaPath,                                                                                      \
+              CNAME,                                                                               \
+              reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>)}
 
 const GemmVariant kGemmVariants[] = {
-    MB_GEMM_DMA(MB_MATRIX_BF16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64"),
+    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64",
+                   "gemm_bf16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
-    MB_GEMM_DMA(MB_MATRIX_F16, MfmaF16, 64, 256, 256, "gemm_f16_256x256x64"),
+    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16, 64, 256, 256, "gemm_f16_256x256x64",
+                   "gemm_f16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM_DMA(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128"),
+    MB_GEMM_DMA(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128",
+                "gemm_fp8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
-    MB_GEMM_DMA(MB_MATRIX_I8, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128"),
+    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128",
+                   "gemm_i8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
-    MB_GEMM_DMA(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 128, "gemm_mxfp4_256x256x256"),
+    MB_GEMM_STAGED(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 128, "gemm_mxfp4_256x256x256",
+                   "gemm_mxfp4_128x128x256_checked"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, "gemm_mxfp4_128x128x256"),
     MB_GEMM(MB_MATRIX_F64, MfmaF64, 128, 128, 16, 2, 2, "gemm_f64_128x128x16"),
@@ -497,7 +714,14 @@ const GemmVariant kGemmVariants[] = {
 
 struct GemmRegistrar {
   GemmRegistrar() {
-    for (const auto& variant : kGemmVariants) register_kernel(variant.name, variant.kernel);
+    for (const auto& variant : kGemmVariants) {
+      register_kernel(variant.name, variant.kernel);
+      // A fallback can be another variant's checked kernel: register each name once.
+      bool seen = false;
+      for (const auto* other = kGemmVariants; other != &variant; ++other)
+        seen = seen || std::strcmp(other->checked_name, variant.checked_name) == 0;
+      if (!seen) register_kernel(variant.checked_name, variant.checked_kernel);
+    }
   }
 };
 const GemmRegistrar kGemmRegistrar;
@@ -510,6 +734,55 @@ const GemmVariant* find_gemm(int format, const mb_gemm_config* config) {
       return &variant;
   }
   return nullptr;
+}
+
+// The launcher (and its registered name) a call will use: the variant's fast
+// kernel when the shape divides its tile and meets the path's rule, else its
+// checked kernel.
+struct GemmChoice {
+  const GemmVariant* variant;
+  GemmLauncher launch;
+  const char* name;
+};
+
+int choose_gemm(int format, const mb_gemm_config* config, uint32_t m, uint32_t n, uint32_t k, const void* scale_a,
+                const void* scale_b, const char* entry, GemmChoice* out) {
+  if (int rc = matrix_format_check(format, entry)) return rc;
+  if (config == nullptr) return fail(MB_ERR_INVALID, "%s: config is NULL", entry);
+  const GemmVariant* variant = find_gemm(format, config);
+  if (variant == nullptr)
+    return fail(MB_ERR_INVALID, "%s: no kernel for format %d with tile %ux%ux%u (see mb_gemm_configs)", entry, format,
+                config->tile_m, config->tile_n, config->tile_k);
+  if (m == 0 || n == 0 || k == 0) return fail(MB_ERR_INVALID, "%s: empty problem %ux%ux%u", entry, m, n, k);
+  if (m > 0x7fffffffu || n > 0x7fffffffu || k > 0x7fffffffu)
+    return fail(MB_ERR_INVALID, "%s: dimensions exceed 2^31-1", entry);
+  if (format == MB_MATRIX_MXFP4 && k % 32)
+    return fail(MB_ERR_INVALID, "%s: MXFP4 needs K to be a multiple of the 32-element scale group", entry);
+  const uint64_t row_bits = static_cast<uint64_t>(k) * variant->elem_bits;
+  if (row_bits % 128)
+    return fail(MB_ERR_INVALID, "%s: K*element size must be a multiple of 16 bytes (rows are 16-byte loads)", entry);
+  // The tile count of the smallest tile any launcher uses bounds the grid.
+  const uint64_t max_tiles = static_cast<uint64_t>((m + 63) / 64) * ((n + 63) / 64);
+  if (max_tiles > 0x7fffffffull) return fail(MB_ERR_INVALID, "%s: too many tiles", entry);
+  const uint64_t row_bytes = row_bits / 8, steps = row_bytes / 128;
+  const mb_gemm_config& v = variant->config;
+  bool fast = m % v.tile_m == 0 && n % v.tile_n == 0 && k % v.tile_k == 0;
+  // The 256x256 kernels address each tile's operand rows (and the staged
+  // kernel the MXFP4 scale blocks) with 32-bit offsets in 128-byte K steps;
+  // the staged kernel runs an even number of at least four steps and moves
+  // scale rows with 16-byte DMAs.
+  if (variant->path != kLdsPath)
+    fast = fast && row_bytes % 128 == 0 && 256 * row_bytes <= 0x7fffffffull;
+  if (variant->path == kStagedPath) {
+    fast = fast && steps >= 4 && steps % 2 == 0;
+    if (format == MB_MATRIX_MXFP4)
+      fast = fast && aligned(scale_a, 16) && aligned(scale_b, 16) &&
+             steps * (m > n ? m : n) * 8 <= 0x7fffffffull;
+  }
+  out->variant = variant;
+  out->launch = fast ? variant->launch : variant->launch_checked;
+  out->name = fast ? variant->name : variant->checked_name;
+  return MB_OK;
 }
 
 }  // namespace
@@ -540,21 +813,10 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
             uint64_t scale_b_bytes, void* c, uint64_t c_bytes, uint32_t m, uint32_t n, uint32_t k,
             uint32_t group_m, void* stream) {
   using namespace mb;
-  if (int rc = matrix_format_check(format, "mb_gemm")) return rc;
-  if (config == nullptr) return fail(MB_ERR_INVALID, "mb_gemm: config is NULL");
-  const GemmVariant* variant = find_gemm(format, config);
-  if (variant == nullptr)
-    return fail(MB_ERR_INVALID, "mb_gemm: no kernel for format %d with tile %ux%ux%u (see mb_gemm_configs)", format,
-                config->tile_m, config->tile_n, config->tile_k);
-  if (m == 0 || n == 0 || k == 0) return fail(MB_ERR_INVALID, "mb_gemm: empty problem %ux%ux%u", m, n, k);
-  if (m > 0x7fffffffu || n > 0x7fffffffu || k > 0x7fffffffu)
-    return fail(MB_ERR_INVALID, "mb_gemm: dimensions exceed 2^31-1");
-  if (format == MB_MATRIX_MXFP4 && k % 32)
-    return fail(MB_ERR_INVALID, "mb_gemm: MXFP4 needs K to be a multiple of the 32-element scale group");
-  const uint64_t row_bits = static_cast<uint64_t>(k) * variant->elem_bits;
-  if (row_bits % 128)
-    return fail(MB_ERR_INVALID, "mb_gemm: K*element size must be a multiple of 16 bytes (rows are 16-byte loads)");
-  const uint64_t row_bytes = row_bits / 8;
+  GemmChoice choice;
+  if (int rc = choose_gemm(format, config, m, n, k, scale_a, scale_b, "mb_gemm", &choice)) return rc;
+  const GemmVariant* variant = choice.variant;
+  const uint64_t row_bytes = static_cast<uint64_t>(k) * variant->elem_bits / 8;
   if (a == nullptr || b == nullptr || c == nullptr) return fail(MB_ERR_INVALID, "mb_gemm: NULL operand");
   if (a_bytes < m * row_bytes || b_bytes < n * row_bytes ||
       c_bytes < static_cast<uint64_t>(m) * n * variant->out_bytes)
@@ -564,26 +826,22 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
   if (format == MB_MATRIX_MXFP4) {
     if (scale_a == nullptr || scale_b == nullptr)
       return fail(MB_ERR_INVALID, "mb_gemm: MXFP4 needs E8M0 scales for A and B");
-    if (scale_a_bytes < static_cast<uint64_t>(m) * (k / 32) || scale_b_bytes < static_cast<uint64_t>(n) * (k / 32))
-      return fail(MB_ERR_INVALID, "mb_gemm: scale buffers too small ([M|N][K/32] bytes needed)");
+    const uint64_t blocks = (k + 255) / 256;
+    if (scale_a_bytes < blocks * m * 8 || scale_b_bytes < blocks * n * 8)
+      return fail(MB_ERR_INVALID, "mb_gemm: scale buffers too small ([ceil(K/256)][M|N][8] bytes needed)");
   }
-  const mb_gemm_config& v = variant->config;
-  const bool exact = m % v.tile_m == 0 && n % v.tile_n == 0 && k % v.tile_k == 0;
-  // The DMA kernel addresses each tile's 256 operand rows with 32-bit offsets.
-  // Its scale rows are moved 4 bytes per lane, so they must be 4-byte aligned.
-  const bool offsets_fit =
-      variant->dma_row_bytes == 0 ||
-      (row_bytes % variant->dma_row_bytes == 0 && 256 * row_bytes <= 0x7fffffffull &&
-       (format != MB_MATRIX_MXFP4 || (aligned(scale_a, 4) && aligned(scale_b, 4))));
-  // The tile count of the smallest tile any launcher uses bounds the grid.
-  const uint64_t max_tiles = static_cast<uint64_t>((m + 63) / 64) * ((n + 63) / 64);
-  if (max_tiles > 0x7fffffffull) return fail(MB_ERR_INVALID, "mb_gemm: too many tiles");
   const int group = group_m ? static_cast<int>(group_m) : 8;
-  GemmLauncher launch = exact && offsets_fit ? variant->launch : variant->launch_checked;
-  launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
-         static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), group,
-         static_cast<hipStream_t>(stream));
-  return launch_status(variant->name);
+  choice.launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
+                static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                group, static_cast<hipStream_t>(stream));
+  return launch_status(choice.name);
+}
+
+const char* mb_gemm_launched_kernel(int format, const mb_gemm_config* config, uint32_t m, uint32_t n, uint32_t k,
+                                    const void* scale_a, const void* scale_b) {
+  mb::GemmChoice choice;
+  if (mb::choose_gemm(format, config, m, n, k, scale_a, scale_b, "mb_gemm_launched_kernel", &choice)) return nullptr;
+  return choice.name;
 }
 
 }  // extern "C"

@@ -28,6 +28,21 @@ def pack_e2m1_pairs(codes):
     return ((high << 4) | (low & 15)).to(torch.uint8)
 
 
+def mx_scale_blocks(scales, fill=E8M0_UNIT_SCALE):
+    """Row-major E8M0 scales [rows][K/32] -> the GEMM's K-step blocks [ceil(K/256)][rows][8].
+
+    Block b, row r, group g holds the scale of row r for K elements
+    256b + 32g .. 256b + 32g + 31; groups past K are `fill`.
+    """
+    import torch
+
+    rows, groups = scales.shape
+    blocks = -(-groups // 8)
+    padded = torch.full((rows, blocks * 8), fill, dtype=torch.uint8, device=scales.device)
+    padded[:, :groups] = scales
+    return padded.view(rows, blocks, 8).permute(1, 0, 2).contiguous()
+
+
 def e2m1_decode(codes):
     """Float64 values of E2M1 codes (any integer tensor of 0..15)."""
     import torch

@@ -46,8 +46,9 @@ def gemm_inputs(dtype: str, m: int, n: int, k: int, device, seed: int = 0):
         codes_a = torch.randint(0, 16, (m, k), device=device, generator=generator, dtype=torch.uint8)
         codes_b = torch.randint(0, 16, (n, k), device=device, generator=generator, dtype=torch.uint8)
         a, b = formats.pack_e2m1_pairs(codes_a), formats.pack_e2m1_pairs(codes_b)
-        scales = (torch.full((m, k // 32), formats.E8M0_UNIT_SCALE, dtype=torch.uint8, device=device),
-                  torch.full((n, k // 32), formats.E8M0_UNIT_SCALE, dtype=torch.uint8, device=device))
+        blocks = -(-k // 256)  # K-step scale blocks [ceil(K/256)][rows][8] (mb_gemm's layout)
+        scales = (torch.full((blocks, m, 8), formats.E8M0_UNIT_SCALE, dtype=torch.uint8, device=device),
+                  torch.full((blocks, n, 8), formats.E8M0_UNIT_SCALE, dtype=torch.uint8, device=device))
         a_values, b_values = formats.e2m1_decode(codes_a), formats.e2m1_decode(codes_b)
         del codes_a, codes_b
     elif dtype == "fp8":
@@ -144,7 +145,8 @@ def run_gemm(args, metadata: dict, device) -> None:
         ref = reference(a_values, b_values)
         del a_values, b_values
         for config in candidates:
-            kernel = _native.gemm_kernel_name(dtype, config)
+            # The kernel this shape actually launches (a ragged shape runs the tile's checked variant).
+            kernel = _native.gemm_launched_kernel(dtype, config, size, size, size, *(scales or (None, None)))
             c.fill_(-2**31 if dtype == "int8" else float("nan"))
 
             def run(config=config):
