@@ -12,24 +12,20 @@
 // row-major; the MI355X kernel takes K-contiguous B (layout prepared outside
 // timing by the caller).
 //
-// Three kernels:
-//   * gemm_staged_kernel: 256x256 tiles of the 16-byte-fragment formats (BF16,
-//     FP16, INT8, MXFP4) when the shape divides the tile. Four waves, one per
-//     SIMD, each owning 128x128 outputs (16 accumulators of 32x32 in AGPRs).
-//     Operands flow global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128
-//     bytes of every row) is loaded two steps ahead into one of two register
-//     sets, written to one of two LDS stages a step ahead, and read back as
-//     fragments one substep ahead. Loads, stage writes and fragment reads are
+// Two kernels:
+//   * gemm_staged_kernel: 256x256 tiles of BF16, FP16, INT8, FP8 and MXFP4
+//     when the shape divides the tile. Four waves, one per SIMD, each owning
+//     128x128 outputs (16 accumulators of 32x32 in AGPRs). Operands flow
+//     global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128 bytes of every
+//     row) is loaded two steps ahead into one of two register sets, written to
+//     one of two LDS stages a step ahead, and read back as fragments ahead of
+//     the MFMAs that use them. Loads, stage writes and fragment reads are
 //     spread across the step's MFMAs, so no burst of memory instructions
 //     stalls the in-order MFMA issue; one barrier per step.
-//   * gemm_dma_kernel: 256x256 FP8 tiles, operands fed straight from L2 into
-//     LDS by buffer_load_dwordx4 ... lds (8 waves, 2 per SIMD), faster for the
-//     32-byte FP8 fragments, whose double buffer does not fit beside the
-//     staged kernel's registers.
 //   * gemm_kernel: every other tile and every ragged shape (CHECKED
 //     instantiations bound each load and store), operands staged through a
 //     padded, double-buffered LDS tile with 16-byte loads.
-// All three number workgroups XCD-first: the hardware deals consecutive ids
+// Both number workgroups XCD-first: the hardware deals consecutive ids
 // round-robin over the 8 XCDs, so id i is remapped to the i/8-th tile of XCD
 // i%8's contiguous share, walked in GROUP_M-row bands that keep A and B panels
 // hot in that XCD's L2.
@@ -222,16 +218,13 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
 
 // One 16-byte-per-lane LDS DMA: lane l's 16 bytes land at lds_addr + 16 * l.
 // Issued as inline assembly so the compiler's wait-count pass does not force a
-// full vmcnt(0) before every LDS read; the kernels wait explicitly instead, or
-// (staged kernel) issue it ahead of compiler-visible loads whose in-order
-// vmcnt waits then cover it.
+// full vmcnt(0) before every LDS read; the staged kernel issues it ahead of
+// compiler-visible loads, whose in-order vmcnt waits then cover it.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, uint32_t lds_addr) {
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
                "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory");
 }
-
-__device__ __forceinline__ void wait_all_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Word 3 of a gfx9 buffer resource: 32-bit data format, no swizzle, raw offsets.
 constexpr int kBufferWord3 = 0x00020000;
@@ -260,140 +253,16 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// ---- DMA-fed 256x256 kernel (FP8) ------------------------------------------
-
-// C = A . B^T for M, N multiples of 256 and K * bits multiples of ROWB * 8;
-// A, B byte offsets must fit in 31 bits. Each K step stages a 256 x ROWB-byte
-// slice of A and of B (one LDS stage, double-buffered). LDS row r holds its
-// 16-byte chunk c at position c ^ ((r / (256 / ROWB)) % (ROWB / 16)): any 16
-// consecutive rows read at one logical chunk hit 16 distinct bank groups.
-template <class Op, int ROWB, int WAVES_M, int WAVES_N>
-__global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
-    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
-                    const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
-                    int group_m) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int BM = 256, BN = 256;
-  constexpr int NW = WAVES_M * WAVES_N;
-  constexpr int CPR = ROWB / 16;      // 16-byte chunks per LDS row
-  constexpr int RPI = 1024 / ROWB;    // rows one DMA instruction fills (64 lanes x 16 bytes)
-  constexpr int RPB = 256 / ROWB;     // rows per 256 bytes: the swizzle period
-  constexpr int STAGE = (BM + BN) * ROWB;
-  constexpr int INSTR = (BM + BN) / RPI / NW;  // DMA instructions per wave per K step
-  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / Op::M, TN = WN / Op::N;
-  constexpr int KB = MfmaGeometry<Op>::K_BYTES, KSTEPS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
-  static_assert(!Op::SCALED, "scaled formats use the staged kernel");
-  static_assert((BM / RPI) % NW == 0, "an instruction's rows are all A or all B, whatever the wave");
-  static_assert(ROWB % KB == 0 && Op::LANE_BYTES % 16 == 0 && Op::M == 32, "whole 32x32 instructions per step");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
-  // The array is otherwise written only by DMA, which the optimizer does not
-  // see as a store; one plain (never executed) store keeps its reads live.
-  if (K < 0) lds[threadIdx.x] = 0;
-
-  int tile_m, tile_n;
-  band_tile(M / BM, N / BN, group_m, tile_m, tile_n);
-  const int m0 = tile_m * BM, n0 = tile_n * BN;
-  const int row_bytes = K * Op::ELEM_BITS / 8;
-  const int k_steps = row_bytes / ROWB;
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // Each resource covers exactly this tile's 256 rows of its operand.
-  const __amdgpu_buffer_rsrc_t rsrc_a = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
-  const __amdgpu_buffer_rsrc_t rsrc_b = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BN * row_bytes);
-  const uint32_t lds_base =
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(lds)));
-  // DMA instruction j of this wave fills LDS rows rb*RPI .. rb*RPI+RPI-1 of the
-  // A|B stage, rb = j*NW + wave; lane l supplies row rb*RPI + l/CPR, physical
-  // chunk l%CPR, i.e. the global chunk that swizzles there.
-  int voff[INSTR];
-#pragma unroll
-  for (int j = 0; j < INSTR; ++j) {
-    const int row = (j * NW + wave) * RPI + lane / CPR;
-    const int chunk = (lane % CPR) ^ ((row / RPB) % CPR);
-    voff[j] = (row < BM ? row : row - BM) * row_bytes + chunk * 16;
+// f(integral_constant<I>) for I = I0 .. N-1, so counts derived from I are constants.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
   }
-  auto issue = [&](int kt) {
-    const uint32_t stage = lds_base + (kt & 1) * STAGE;
-#pragma unroll
-    for (int j = 0; j < INSTR; ++j) {
-      const uint32_t dst = stage + (j * NW + wave) * 1024;
-      if (j * NW < BM / RPI) dma16(rsrc_a, voff[j], kt * ROWB, dst);
-      else dma16(rsrc_b, voff[j], kt * ROWB, dst);
-    }
-  };
-
-  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
-  const int lrow = lane & 31, lgroup = lane >> 5;
-  typename Op::Acc acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = typename Op::Acc{};
-
-  // Fragment of LDS row `row` for substep ks: LANE_BYTES from logical chunks
-  // ks*KB/16 + lgroup*PIECES + p.
-  auto read = [&](const uint8_t* stage, int row, int ks) {
-    i32x4 parts[PIECES];
-#pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int c = ks * (KB / 16) + lgroup * PIECES + p;
-      parts[p] = *reinterpret_cast<const i32x4*>(stage + row * ROWB + ((c ^ ((row / RPB) % CPR)) * 16));
-    }
-    if constexpr (PIECES == 1) {
-      return __builtin_bit_cast(typename Op::Frag, parts[0]);
-    } else {
-      return typename Op::Frag{parts[0][0], parts[0][1], parts[0][2], parts[0][3],
-                               parts[1][0], parts[1][1], parts[1][2], parts[1][3]};
-    }
-  };
-
-  issue(0);
-  for (int kt = 0; kt < k_steps; ++kt) {
-    // Step kt's DMA is complete for this wave; the barrier makes every wave's
-    // part visible and ends all reads of the other stage, which the next DMA
-    // then overwrites.
-    wait_all_dma();
-    __syncthreads();
-    if (kt + 1 < k_steps) issue(kt + 1);
-    const uint8_t* stage = lds + (kt & 1) * STAGE;
-    typename Op::Frag fa[2][TM], fb[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[0][i] = read(stage, wm * WM + i * 32 + lrow, 0);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[0][j] = read(stage, BM + wn * WN + j * 32 + lrow, 0);
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < KSTEPS) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) fa[cur ^ 1][i] = read(stage, wm * WM + i * 32 + lrow, ks + 1);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) fb[cur ^ 1][j] = read(stage, BM + wn * WN + j * 32 + lrow, ks + 1);
-      }
-      // Keep the next substep's reads ahead of this substep's MFMAs.
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = Op::mma(fa[cur][i], fb[cur][j], acc[i][j], 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < Op::ACC_REGS; ++r) {
-        const int row = m0 + wm * WM + i * 32 + Op::out_row(lane, r);
-        const int col = n0 + wn * WN + j * 32 + lrow;
-        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
-      }
-#endif
 }
 
-// ---- VGPR-staged 256x256 kernel (BF16, FP16, INT8, MXFP4) -------------------
+// ---- VGPR-staged 256x256 kernel (BF16, FP16, INT8, FP8, MXFP4) --------------
 
 // C = A . B^T for M, N multiples of 256, K * bits a multiple of 1024 (128-byte
 // K steps) with an even number of at least 4 steps; A, B byte offsets and the
@@ -421,9 +290,10 @@ __global__ void __launch_bounds__(256)
                        typename Op::Out* __restrict__ C, int M, int N, int K, int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NL = 16;
-  constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB;
+  constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
   constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = Op::SCALED ? 4 : 0;
-  static_assert(Op::M == 32 && Op::LANE_BYTES == 16 && KS == 4, "16-byte 32x32 fragments, four substeps");
+  static_assert(Op::M == 32 && ((PIECES == 1 && KS == 4) || (PIECES == 2 && KS == 2 && !Op::SCALED)),
+                "16-byte fragments in four substeps, or unscaled 32-byte fragments in two");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * REGION + SCALE_RING * SCALE_STAGE];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written (scale) reads live; never executed
 
@@ -476,10 +346,11 @@ __global__ void __launch_bounds__(256)
 
   const int wm = wave & 1, wn = wave >> 1;
   const int lrow = lane & 31, lgroup = lane >> 5;
-  // A lane's fragment of substep ks is its row's logical chunk 2ks + lgroup,
-  // i.e. the lane base XOR (ks << 5): only address bits 5..6 change, so
-  // region, stage and fragment offsets still add as immediates.
-  const int sw = ((lrow >> 1) & 7) ^ lgroup;
+  // Piece p of a lane's fragment of substep ks is its row's logical chunk
+  // ks*KB/16 + lgroup*PIECES + p, i.e. the lane base XOR ((ks*KB/16 + p) << 4):
+  // only address bits 4..6 change, so region, stage and fragment offsets still
+  // add as immediates.
+  const int sw = ((lrow >> 1) & 7) ^ (lgroup * PIECES);
   const uint32_t ra_off = (wm * 128 + lrow) * ROWB + (sw << 4);
   const uint32_t rb_off = 2 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
   using Frag8 = i32x4[8];
@@ -517,8 +388,6 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < 4; ++j) acc[i][j] = typename Op::Acc{};
 
   i32x4 v0[NL], v1[NL];
-  Frag8 fa, fb;
-  Scales8 sa0, sa1;
   // Prologue: steps 0 and 1 in flight, step 0 into stage 0, step 2 into v0.
   // The wait for v0 before its stage write also covers the older scale DMAs.
   scale_dma(0, 0);
@@ -529,60 +398,125 @@ __global__ void __launch_bounds__(256)
   store(v0, 0, 0, NL);
   load(v0, 2, 0, NL);
   lds_barrier();
-  read(fa, 0, 0);
-  read_scales(sa0, 0);
 
-  auto step = [&](int kt, int s, i32x4 (&vnext)[NL], Scales8& sc, Scales8& sc_next) __attribute__((always_inline)) {
-    auto substep = [&](auto ks_c) __attribute__((always_inline)) {
-      constexpr int ks = decltype(ks_c)::value;
-      Frag8& cur = (ks & 1) ? fb : fa;
-      Frag8& nxt = (ks & 1) ? fa : fb;
-      if constexpr (ks + 1 < KS) {
-        read(nxt, s, ks + 1);
-      } else {
-        read(nxt, s ^ 1, 0);
-        read_scales(sc_next, kt + 1);
-      }
-      // This substep's share of step kt+1's stage writes (all before the
-      // barrier) and of step kt+3's loads, each behind the write that frees
-      // its registers; the scale DMA of step kt+3 goes first, so the in-order
-      // waits for these loads cover it.
-      constexpr int W0 = ks * NL / (KS - 1) < NL ? ks * NL / (KS - 1) : NL;
-      constexpr int W1 = (ks + 1) * NL / (KS - 1) < NL ? (ks + 1) * NL / (KS - 1) : NL;
-      constexpr int L0 = ks * NL / KS, L1 = (ks + 1) * NL / KS;
-      store(vnext, s ^ 1, W0, W1);
-      if constexpr (ks == 0) scale_dma(kt + 3, min(kt + 3, last));
-      load(vnext, min(kt + 3, last), L0, L1);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (Op::SCALED)
-            acc[i][j] = Op::template mma_byte<ks>(cur[i], cur[4 + j], acc[i][j], sc[i], sc[4 + j]);
-          else
-            acc[i][j] = Op::mma(cur[i], cur[4 + j], acc[i][j], 0, 0);
+  if constexpr (PIECES == 1) {
+    // 16-byte fragments: A and B fragments of a substep double-buffered (fa/fb).
+    Frag8 fa, fb;
+    Scales8 sa0, sa1;
+    read(fa, 0, 0);
+    read_scales(sa0, 0);
+    auto step = [&](int kt, int s, i32x4 (&vnext)[NL], Scales8& sc, Scales8& sc_next) __attribute__((always_inline)) {
+      auto substep = [&](auto ks_c) __attribute__((always_inline)) {
+        constexpr int ks = decltype(ks_c)::value;
+        Frag8& cur = (ks & 1) ? fb : fa;
+        Frag8& nxt = (ks & 1) ? fa : fb;
+        if constexpr (ks + 1 < KS) {
+          read(nxt, s, ks + 1);
+        } else {
+          read(nxt, s ^ 1, 0);
+          read_scales(sc_next, kt + 1);
         }
-      // Interleave: after each MFMA, one of the next substep's fragment reads
-      // (front-loaded) and this substep's writes and loads, evenly spaced.
-      constexpr int WR = W1 - W0, LD = L1 - L0;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // MFMA
-        if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                         // DS read
-        if ((q + 1) * WR / 16 != q * WR / 16) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-        if ((q + 1) * LD / 16 != q * LD / 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-      }
-      if constexpr (ks == KS - 2) lds_barrier();
-      __builtin_amdgcn_sched_barrier(0);
+        // This substep's share of step kt+1's stage writes (all before the
+        // barrier) and of step kt+3's loads, each behind the write that frees
+        // its registers; the scale DMA of step kt+3 goes first, so the in-order
+        // waits for these loads cover it.
+        constexpr int W0 = ks * NL / (KS - 1) < NL ? ks * NL / (KS - 1) : NL;
+        constexpr int W1 = (ks + 1) * NL / (KS - 1) < NL ? (ks + 1) * NL / (KS - 1) : NL;
+        constexpr int L0 = ks * NL / KS, L1 = (ks + 1) * NL / KS;
+        store(vnext, s ^ 1, W0, W1);
+        if constexpr (ks == 0) scale_dma(kt + 3, min(kt + 3, last));
+        load(vnext, min(kt + 3, last), L0, L1);
+  #pragma unroll
+        for (int i = 0; i < 4; ++i)
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if constexpr (Op::SCALED)
+              acc[i][j] = Op::template mma_byte<ks>(cur[i], cur[4 + j], acc[i][j], sc[i], sc[4 + j]);
+            else
+              acc[i][j] = Op::mma(cur[i], cur[4 + j], acc[i][j], 0, 0);
+          }
+        // Interleave: after each MFMA, one of the next substep's fragment reads
+        // (front-loaded) and this substep's writes and loads, evenly spaced.
+        constexpr int WR = W1 - W0, LD = L1 - L0;
+  #pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // MFMA
+          if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                         // DS read
+          if ((q + 1) * WR / 16 != q * WR / 16) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+          if ((q + 1) * LD / 16 != q * LD / 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+        }
+        if constexpr (ks == KS - 2) lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      substep(std::integral_constant<int, 0>{});
+      substep(std::integral_constant<int, 1>{});
+      substep(std::integral_constant<int, 2>{});
+      substep(std::integral_constant<int, 3>{});
     };
-    substep(std::integral_constant<int, 0>{});
-    substep(std::integral_constant<int, 1>{});
-    substep(std::integral_constant<int, 2>{});
-    substep(std::integral_constant<int, 3>{});
-  };
-  for (int kt = 0; kt < k_steps; kt += 2) {
-    step(kt, 0, v1, sa0, sa1);
-    step(kt + 1, 1, v0, sa1, sa0);
+    for (int kt = 0; kt < k_steps; kt += 2) {
+      step(kt, 0, v1, sa0, sa1);
+      step(kt + 1, 1, v0, sa1, sa0);
+    }
+  } else {
+    // 32-byte fragments (two substeps per step): A fragments double-buffered,
+    // B fragments in one set, B_j refilled with the next substep's B_j right
+    // after the four MFMAs that read it (a column). Each column is fenced so
+    // the refill cannot be hoisted above the MFMAs still reading the old B_j,
+    // and the column's share of the next A reads, stage writes and loads is
+    // interleaved with its MFMAs.
+    using F = typename Op::Frag;
+    F fa0[4], fa1[4], fbq[4];
+    auto read_frag = [&](uint32_t off, int s, int ks, int f) __attribute__((always_inline)) {
+      const uint32_t x0 = static_cast<uint32_t>(ks * (KB / 16)) << 4, x1 = x0 + 16;
+      const i32x4 lo = *reinterpret_cast<const i32x4*>(lds + (off ^ x0) + s * REGION + f * 32 * ROWB);
+      const i32x4 hi = *reinterpret_cast<const i32x4*>(lds + (off ^ x1) + s * REGION + f * 32 * ROWB);
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      fa0[f] = read_frag(ra_off, 0, 0, f);
+      fbq[f] = read_frag(rb_off, 0, 0, f);
+    }
+    auto step = [&](int kt, int s, i32x4 (&vnext)[NL]) __attribute__((always_inline)) {
+      static_for<0, KS>([&](auto ks_c) __attribute__((always_inline)) {
+        constexpr int ks = decltype(ks_c)::value;
+        F (&cur)[4] = (ks & 1) ? fa1 : fa0;
+        F (&nxt)[4] = (ks & 1) ? fa0 : fa1;
+        const int ns = ks + 1 < KS ? s : s ^ 1, nks = ks + 1 < KS ? ks + 1 : 0;
+        constexpr int W0 = ks == 0 ? 0 : NL, W1 = NL;  // all stage writes before the barrier
+        constexpr int L0 = ks * NL / KS, L1 = (ks + 1) * NL / KS;
+        static_for<0, 4>([&](auto j_c) __attribute__((always_inline)) {
+          constexpr int j = decltype(j_c)::value;
+          constexpr int CW0 = W0 + (W1 - W0) * j / 4, CW1 = W0 + (W1 - W0) * (j + 1) / 4;
+          constexpr int CL0 = L0 + (L1 - L0) * j / 4, CL1 = L0 + (L1 - L0) * (j + 1) / 4;
+          if constexpr (j == 0) {
+#pragma unroll
+            for (int f = 0; f < 4; ++f) nxt[f] = read_frag(ra_off, ns, nks, f);
+          }
+          store(vnext, s ^ 1, CW0, CW1);
+          load(vnext, min(kt + 3, last), CL0, CL1);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i][j] = Op::mma(cur[i], fbq[j], acc[i][j], 0, 0);
+          constexpr int RA = j == 0 ? 8 : 0, WR = CW1 - CW0, LD = CL1 - CL0;
+          static_for<0, 4>([&](auto q_c) __attribute__((always_inline)) {
+            constexpr int q = decltype(q_c)::value;
+            constexpr int NW = (q + 1) * WR / 4 - q * WR / 4, NLD = (q + 1) * LD / 4 - q * LD / 4;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
+            if constexpr (RA > 0) __builtin_amdgcn_sched_group_barrier(0x100, RA / 4, 0);  // DS read
+            if constexpr (NW > 0) __builtin_amdgcn_sched_group_barrier(0x200, NW, 0);      // DS write
+            if constexpr (NLD > 0) __builtin_amdgcn_sched_group_barrier(0x020, NLD, 0);    // VMEM read
+          });
+          __builtin_amdgcn_sched_barrier(0);
+          fbq[j] = read_frag(rb_off, ns, nks, j);
+        });
+        if constexpr (ks == KS - 2) lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
+    for (int kt = 0; kt < k_steps; kt += 2) {
+      step(kt, 0, v1);
+      step(kt + 1, 1, v0);
+    }
   }
 
 #pragma unroll
@@ -613,13 +547,6 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
-template <class Op, int ROWB, int WM, int WN>
-void launch_gemm_dma(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m, int n,
-                     int k, int group_m, hipStream_t stream) {
-  gemm_dma_kernel<Op, ROWB, WM, WN><<<dim3(tile_count(m, n, 256, 256)), dim3(64 * WM * WN), 0, stream>>>(
-      a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
-}
-
 template <class Op>
 void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m,
                         int n, int k, int group_m, hipStream_t stream) {
@@ -628,7 +555,7 @@ void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, c
 }
 
 // What a variant's fast launcher needs beyond a shape that divides its tile.
-enum GemmPath { kLdsPath = 0, kDmaPath = 1, kStagedPath = 2 };
+enum GemmPath { kLdsPath = 0, kStagedPath = 1 };
 
 // launch: shapes that divide the tile and satisfy the path's rule (see
 // exact_shape); launch_checked: any shape.
@@ -659,8 +586,8 @@ struct GemmVariant {
               NAME "_checked",                                                                               \
               reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, true>)}
 
-// 256x256 tiles: the staged kernel (BK = 128 bytes of K) or, for FP8, the DMA
-// kernel for exact shapes; a checked LDS-staged kernel (tile CM x CN) for the rest.
+// 256x256 tiles: the staged kernel (BK = 128 bytes of K) for exact shapes, a
+// checked LDS-staged kernel (tile CM x CN) for the rest.
 #define MB_GEMM_STAGED(FMT, OP, BK, CM, CN, NAME, CNAME)                                                          \
   GemmVariant{FMT,                                                                                           \
               mb_gemm_config{256, 256, BK, 256},                                                             \
@@ -673,19 +600,6 @@ struct GemmVariant {
               kStagedPath,                                                                                   \
               CNAME,                                                                               \
               reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>)}
-#define MB_GEMM_DMA(FMT, OP, BK, CM, CN, NAME, CNAME)                                                          \
-  GemmVariant{FMT,                                                                                           \
-              mb_gemm_config{256, 256, BK, 512},                                                             \
-              NAME,                                                                                          \
-              reinterpret_cast<const void*>(gemm_dma_kernel<OP, 128, 2, 4>),                                 \
-              launch_gemm_dma<OP, 128, 2, 4>,                                                                \
-              launch_gemm<OP, CM, CN, BK, 2, 2, true>,                                                       \
-              static_cast<int>(sizeof(typename OP::Out)),                                                    \
-              OP::ELEM_BITS,                                                                                 \
-              kDmaPath,                                                                                      \
-              CNAME,                                                                               \
-              reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>)}
-
 const GemmVariant kGemmVariants[] = {
     MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64",
                    "gemm_bf16_256x256x64_checked"),
@@ -695,8 +609,8 @@ const GemmVariant kGemmVariants[] = {
                    "gemm_f16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM_DMA(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128",
-                "gemm_fp8_256x256x128_checked"),
+    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128",
+                   "gemm_fp8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
     MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128",
@@ -767,14 +681,11 @@ int choose_gemm(int format, const mb_gemm_config* config, uint32_t m, uint32_t n
   const uint64_t row_bytes = row_bits / 8, steps = row_bytes / 128;
   const mb_gemm_config& v = variant->config;
   bool fast = m % v.tile_m == 0 && n % v.tile_n == 0 && k % v.tile_k == 0;
-  // The 256x256 kernels address each tile's operand rows (and the staged
-  // kernel the MXFP4 scale blocks) with 32-bit offsets in 128-byte K steps;
-  // the staged kernel runs an even number of at least four steps and moves
-  // scale rows with 16-byte DMAs.
-  if (variant->path != kLdsPath)
-    fast = fast && row_bytes % 128 == 0 && 256 * row_bytes <= 0x7fffffffull;
+  // The staged kernel addresses each tile's operand rows (and the MXFP4 scale
+  // blocks) with 32-bit offsets in 128-byte K steps, runs an even number of
+  // at least four steps and moves scale rows with 16-byte DMAs.
   if (variant->path == kStagedPath) {
-    fast = fast && steps >= 4 && steps % 2 == 0;
+    fast = fast && row_bytes % 128 == 0 && 256 * row_bytes <= 0x7fffffffull && steps >= 4 && steps % 2 == 0;
     if (format == MB_MATRIX_MXFP4)
       fast = fast && aligned(scale_a, 16) && aligned(scale_b, 16) &&
              steps * (m > n ? m : n) * 8 <= 0x7fffffffull;
