@@ -418,17 +418,15 @@ __global__ void __launch_bounds__(256)
         }
         // This substep's share of step kt+1's stage writes (all before the
         // barrier) and of step kt+3's loads, each behind the write that frees
-        // its registers; the scale DMA of step kt+3 goes first, so the in-order
-        // waits for these loads cover it.
+        // its registers.
         constexpr int W0 = ks * NL / (KS - 1) < NL ? ks * NL / (KS - 1) : NL;
         constexpr int W1 = (ks + 1) * NL / (KS - 1) < NL ? (ks + 1) * NL / (KS - 1) : NL;
         constexpr int L0 = ks * NL / KS, L1 = (ks + 1) * NL / KS;
         store(vnext, s ^ 1, W0, W1);
-        if constexpr (ks == 0) scale_dma(kt + 3, min(kt + 3, last));
         load(vnext, min(kt + 3, last), L0, L1);
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < 4; ++i)
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 4; ++j) {
             if constexpr (Op::SCALED)
               acc[i][j] = Op::template mma_byte<ks>(cur[i], cur[4 + j], acc[i][j], sc[i], sc[4 + j]);
@@ -436,15 +434,21 @@ __global__ void __launch_bounds__(256)
               acc[i][j] = Op::mma(cur[i], cur[4 + j], acc[i][j], 0, 0);
           }
         // Interleave: after each MFMA, one of the next substep's fragment reads
-        // (front-loaded) and this substep's writes and loads, evenly spaced.
-        constexpr int WR = W1 - W0, LD = L1 - L0;
-  #pragma unroll
+        // (front-loaded; in the last substep also the next step's scale rows)
+        // and this substep's writes and loads, evenly spaced.
+        constexpr int WR = W1 - W0, LD = L1 - L0, RD = (Op::SCALED && ks == KS - 1) ? 16 : 8;
+#pragma unroll
         for (int q = 0; q < 16; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // MFMA
-          if (q < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                         // DS read
+          if (q < RD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // DS read
           if ((q + 1) * WR / 16 != q * WR / 16) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
           if ((q + 1) * LD / 16 != q * LD / 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
         }
+        // The scale DMA of step kt+3 (an inline-asm scheduling boundary) goes
+        // after this substep's work; its data is covered by the in-order waits
+        // for step kt+3's loads issued later, which the stage writes of step
+        // kt+2 wait for before the barrier that publishes those scales.
+        if constexpr (ks == 0) scale_dma(kt + 3, min(kt + 3, last));
         if constexpr (ks == KS - 2) lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
       };

@@ -103,11 +103,14 @@ struct MfmaMxfp4 {
     const i32x8 wb = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, wb, c, 4, 4, 0, scale_a, 0, scale_b);
   }
-  // Byte `sel` of two dwords holding one scale per byte (shifted into byte 0, which the
-  // instruction reads).
+  // Scales from byte SEL of two dwords that hold one E8M0 scale per byte: the
+  // instruction's op_sel picks the byte, so no shift is issued.
   template <int SEL>
   __device__ static __forceinline__ Acc mma_byte(Frag a, Frag b, Acc c, uint32_t scales_a, uint32_t scales_b) {
-    return mma(a, b, c, static_cast<int>(scales_a >> (8 * SEL)), static_cast<int>(scales_b >> (8 * SEL)));
+    const i32x8 wa = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+    const i32x8 wb = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa, wb, c, 4, 4, SEL, static_cast<int>(scales_a), SEL,
+                                                           static_cast<int>(scales_b));
   }
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
 };
