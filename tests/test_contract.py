@@ -410,3 +410,40 @@ def test_measured_rows_carry_the_host_baseline_and_the_table_lists_it():
     assert "cpu_baseline" not in declared
     table = format_table([row, declared])
     assert "Host CPU baseline" in table and "Test CPU" in table and "torch.matmul" in table
+
+
+@pytest.mark.parametrize("block", [256, 1024])
+def test_read_check_agrees_with_the_oracle_on_whole_and_tail_blocks(block):
+    """bench_bandwidth.check_read (run on CPU tensors) and oracle.memory.check_read give the same
+    verdict: exact sums pass, and an error just past the bound fails in a whole block, in the
+    partial tail block, and as NaN."""
+    import numpy as np
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import check_read
+
+    rng = np.random.default_rng(block)
+    values = rng.uniform(-1, 1, 7 * block + 37).astype(np.float32)
+    sums = om.block_sums(values, block)
+    bound = om.read_tolerance(values, block)
+
+    def verdicts(sink):
+        product = oracle = True
+        try:
+            check_read(torch.from_numpy(values), torch.from_numpy(sink.astype(np.float32)), block)
+        except AssertionError:
+            product = False
+        try:
+            om.check_read(values, sink.astype(np.float32), block)
+        except AssertionError:
+            oracle = False
+        return product, oracle
+
+    assert verdicts(sums) == (True, True)
+    for index in (2, len(sums) - 1):  # a whole block, then the partial tail block
+        broken = sums.copy()
+        broken[index] += 4 * bound[index]
+        assert verdicts(broken) == (False, False)
+    broken = sums.copy()
+    broken[1] = np.nan
+    assert verdicts(broken) == (False, False)

@@ -155,162 +155,198 @@ MAX_BATCH_LAUNCHES = 2048
 MIN_RESOLVED_EVENT_TICKS = 20
 
 
-class _Timer:
-    """Event pair on the current stream; elapsed device time of one submission."""
+class _EventClock:
+    """Device time of one submission, between two HIP events on the current stream."""
 
     def __init__(self, torch):
         self.torch = torch
-        self.start = torch.cuda.Event(enable_timing=True)
+        self.begin = torch.cuda.Event(enable_timing=True)
         self.end = torch.cuda.Event(enable_timing=True)
 
-    def elapsed(self, submit) -> float:
-        self.start.record()
+    def time(self, submit) -> float:
+        self.begin.record()
         submit()
         self.end.record()
         self.torch.cuda.synchronize()
-        elapsed = float(self.start.elapsed_time(self.end))
-        if not math.isfinite(elapsed) or elapsed < 0:
+        elapsed = float(self.begin.elapsed_time(self.end))
+        if not (math.isfinite(elapsed) and elapsed >= 0):
             raise RuntimeError(f"Invalid device event time: {elapsed!r} ms")
         return elapsed
 
 
-def _zero_event_error(launches=None):
-    workload = f" for {launches} launches" if launches is not None else ""
-    return RuntimeError(f"Invalid device event time: 0 ms{workload}; events are too coarse for this workload")
+class _Submitter:
+    """Callables that issue `count` launches of fn: a captured HIP graph's replay, or direct launches.
 
+    Captured graphs stay cached (alive) for the life of the sampler, since a
+    replay may still be in flight when a new batch size is captured.
+    """
 
-def _coarse_event_error(launches, elapsed_ms, required_ms):
-    return RuntimeError(f"Device event resolution is too coarse: {launches} launches measured {elapsed_ms:g} ms, "
-                        f"but at least {required_ms:g} ms is needed for a reliable peak measurement")
+    def __init__(self, torch, fn, use_graph: bool):
+        self.torch, self.fn, self.use_graph = torch, fn, use_graph
+        self.graphs = {}
 
-
-def _batch_samples(fn, args, use_graph):
-    torch = _torch()
-    stream = torch.cuda.Stream()  # default priority
-    with torch.cuda.stream(stream):
-        timer = _Timer(torch)
-
-        def direct(count):
+    def direct(self, count):
+        def submit():
             for _ in range(count):
-                fn()
+                self.fn()
+        return submit
 
-        # Calibrate: grow the batch until the event pair resolves it.
-        launches, saw_zero = INITIAL_CALIBRATION_LAUNCHES, False
-        while True:
-            elapsed = timer.elapsed(lambda: direct(launches))
-            if elapsed > 0:
-                break
-            if launches == MAX_BATCH_LAUNCHES:
-                raise _zero_event_error(launches)
-            saw_zero, launches = True, min(MAX_BATCH_LAUNCHES, launches * 2)
-        calibration_launches = launches
-        estimate_ms = max(elapsed / launches, 0.001)
-        minimum_launches = launches if saw_zero else 1
-        minimum_batch_ms = elapsed * MIN_RESOLVED_EVENT_TICKS if saw_zero else 0.0
-        target_ms = min(args.batch_ms, args.rep / args.rounds)
-        launches = max(minimum_launches, min(MAX_BATCH_LAUNCHES, math.ceil(target_ms / estimate_ms)))
-        graphs = []  # keep captured graphs alive while their replays may run
-
-        def build_submit(count):
-            if not use_graph:
-                return lambda: direct(count)
+    def __call__(self, count):
+        if not self.use_graph:
+            return self.direct(count)
+        if count not in self.graphs:
             try:
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    direct(count)
+                graph = self.torch.cuda.CUDAGraph()
+                with self.torch.cuda.graph(graph):
+                    self.direct(count)()
             except RuntimeError as exc:
                 raise GraphUnavailable(f"HIP graph capture: {exc}") from exc
-            graphs.append(graph)
-            return graph.replay
+            self.graphs[count] = graph
+        return self.graphs[count].replay
 
-        def time_batch(count, zero_seen=False):
-            nonlocal minimum_batch_ms
-            while True:
-                submit = build_submit(count)
-                elapsed = timer.elapsed(submit)
-                if elapsed > 0 and zero_seen and minimum_batch_ms == 0:
-                    minimum_batch_ms = elapsed * MIN_RESOLVED_EVENT_TICKS
-                if elapsed > 0 and elapsed >= minimum_batch_ms:
-                    return count, submit, elapsed
-                if count == MAX_BATCH_LAUNCHES:
-                    error = (_zero_event_error(count) if elapsed == 0 else
-                             _coarse_event_error(count, elapsed, minimum_batch_ms))
-                    if use_graph:
-                        raise GraphUnavailable(f"HIP graph timing: {error}")
-                    raise error
-                zero_seen = zero_seen or elapsed == 0
-                count = min(MAX_BATCH_LAUNCHES, count * 2)
 
-        launches, submit, batch_ms = time_batch(launches)
-        for _ in range(2):
-            refined = max(minimum_launches,
-                          min(MAX_BATCH_LAUNCHES, math.ceil(launches * target_ms / batch_ms)))
-            if refined == launches or 0.5 * target_ms <= batch_ms <= 2 * target_ms:
+class _Sampler:
+    """Batch-average device time per launch, the reference's measurement policy (common.py:394-534).
+
+    1. Probe: direct launches, doubling from INITIAL_CALIBRATION_LAUNCHES until
+       the event pair resolves them. If a probe read 0 ms the timer is coarse:
+       its first positive reading counts as one tick and every batch must then
+       span MIN_RESOLVED_EVENT_TICKS of them (and at least the probe's launches).
+    2. Size: launches per batch for min(batch_ms, rep / rounds), corrected at
+       most twice while a measured batch is off that target by more than 2x.
+    3. Warm: whole batches for at least --warmup ms.
+    4. Sample: at least --rounds batches and --rep ms. A batch that reads 0 or
+       under the floor doubles the batch size and restarts the sampling, so all
+       samples share one denominator.
+    """
+
+    def __init__(self, torch, fn, args, use_graph: bool):
+        self.torch, self.args, self.use_graph = torch, args, use_graph
+        self.clock = _EventClock(torch)
+        self.batches = _Submitter(torch, fn, use_graph)
+        self.floor_ms = 0.0
+        self.min_launches = 1
+        self.coarse = False
+
+    def _failure(self, launches, elapsed):
+        if elapsed == 0:
+            error = RuntimeError(f"Invalid device event time: 0 ms for {launches} launches; "
+                                 "events are too coarse for this workload")
+        else:
+            error = RuntimeError(f"Device event resolution is too coarse: {launches} launches measured "
+                                 f"{elapsed:g} ms, but at least {self.floor_ms:g} ms is needed for a "
+                                 "reliable peak measurement")
+        return GraphUnavailable(f"HIP graph timing: {error}") if self.use_graph else error
+
+    def probe(self):
+        launches = INITIAL_CALIBRATION_LAUNCHES
+        while True:
+            elapsed = self.clock.time(self.batches.direct(launches))
+            if elapsed > 0:
                 break
-            graphs.clear()
-            launches, submit, batch_ms = time_batch(refined)
+            if launches >= MAX_BATCH_LAUNCHES:
+                raise RuntimeError(f"Invalid device event time: 0 ms for {launches} launches; "
+                                   "events are too coarse for this workload")
+            self.coarse, launches = True, min(MAX_BATCH_LAUNCHES, 2 * launches)
+        if self.coarse:
+            self.floor_ms, self.min_launches = elapsed * MIN_RESOLVED_EVENT_TICKS, launches
+        return launches, max(elapsed / launches, 0.001)
+
+    def resolve(self, launches):
+        """(launches, submit, ms) of the first batch size from `launches` up whose time resolves."""
+        while True:
+            submit = self.batches(launches)
+            elapsed = self.clock.time(submit)
+            if elapsed == 0 and not self.coarse:
+                self.coarse = True  # floor set by the next positive reading
+            elif elapsed > 0 and self.coarse and self.floor_ms == 0:
+                self.floor_ms = elapsed * MIN_RESOLVED_EVENT_TICKS
+            if elapsed > 0 and elapsed >= self.floor_ms:
+                return launches, submit, elapsed
+            if launches >= MAX_BATCH_LAUNCHES:
+                raise self._failure(launches, elapsed)
+            launches = min(MAX_BATCH_LAUNCHES, 2 * launches)
+
+    def bounded(self, launches):
+        return max(self.min_launches, min(MAX_BATCH_LAUNCHES, launches))
+
+    def run(self):
+        args = self.args
+        probe_launches, per_launch = self.probe()
+        target = min(args.batch_ms, args.rep / args.rounds)
+        launches, submit, batch_ms = self.resolve(self.bounded(math.ceil(target / per_launch)))
+        for _ in range(2):
+            if 0.5 * target <= batch_ms <= 2 * target:
+                break
+            resized = self.bounded(math.ceil(launches * target / batch_ms))
+            if resized == launches:
+                break
+            launches, submit, batch_ms = self.resolve(resized)
         for _ in range(max(1, math.ceil(args.warmup / batch_ms))):
             submit()
-        torch.cuda.synchronize()
-        rounds = max(args.rounds, math.ceil(args.rep / batch_ms))
-        batches = []
-        while len(batches) < rounds:
-            elapsed = timer.elapsed(submit)
-            if elapsed > 0 and elapsed >= minimum_batch_ms:
-                batches.append(elapsed)
+        self.torch.cuda.synchronize()
+        samples = []
+        wanted = max(args.rounds, math.ceil(args.rep / batch_ms))
+        while len(samples) < wanted:
+            elapsed = self.clock.time(submit)
+            if elapsed > 0 and elapsed >= self.floor_ms:
+                samples.append(elapsed)
                 continue
-            if launches == MAX_BATCH_LAUNCHES:
-                error = (_zero_event_error(launches) if elapsed == 0 else
-                         _coarse_event_error(launches, elapsed, minimum_batch_ms))
-                if use_graph:
-                    raise GraphUnavailable(f"HIP graph timing: {error}")
-                raise error
-            graphs.clear()
-            launches, submit, batch_ms = time_batch(min(MAX_BATCH_LAUNCHES, launches * 2),
-                                                    zero_seen=elapsed == 0)
-            rounds = max(args.rounds, math.ceil(args.rep / batch_ms))
-            batches.clear()
-        torch.cuda.synchronize()
-    return [elapsed / launches for elapsed in batches], {
-        "launches_per_batch": launches, "batch_samples_ms": batches,
-        "sample_count": len(batches), "measured_total_ms": sum(batches),
-        "graph_api": "torch.cuda.CUDAGraph (HIP graph)" if use_graph else None,
-        "calibration_launches": calibration_launches,
-        "minimum_resolved_batch_ms": minimum_batch_ms,
-    }
+            if launches >= MAX_BATCH_LAUNCHES:
+                raise self._failure(launches, elapsed)
+            if elapsed == 0 and self.floor_ms == 0:
+                self.coarse = True
+            launches, submit, batch_ms = self.resolve(min(MAX_BATCH_LAUNCHES, 2 * launches))
+            wanted = max(args.rounds, math.ceil(args.rep / batch_ms))
+            samples = []
+        self.torch.cuda.synchronize()
+        return [ms / launches for ms in samples], {
+            "launches_per_batch": launches, "batch_samples_ms": samples, "sample_count": len(samples),
+            "measured_total_ms": sum(samples),
+            "graph_api": "torch.cuda.CUDAGraph (HIP graph)" if self.use_graph else None,
+            "calibration_launches": probe_launches, "minimum_resolved_batch_ms": self.floor_ms,
+        }
+
+
+def _sample(fn, args, use_graph):
+    torch = _torch()
+    with torch.cuda.stream(torch.cuda.Stream()):  # a private stream at the default priority
+        return _Sampler(torch, fn, args, use_graph).run()
 
 
 def measure(fn, args):
-    """Device-event timing of `fn` (one kernel launch); never the host clock."""
+    """Device-event timing of `fn` (one kernel launch); never the host clock.
+
+    --timing graph or auto time HIP-graph replays; auto falls back to direct
+    event batches (recording why) when capture or graph timing is unusable.
+    """
     torch = _torch()
-    fn()  # first launch outside any capture or timed sample
+    fn()  # one launch outside any capture or timed sample
     torch.cuda.synchronize()
     requested = args.timing
-    selected = "events" if requested == "events" else "graph"
-    fallback = None
-    if selected == "graph":
+    method, fallback = ("events" if requested == "events" else "graph"), None
+    if method == "graph":
         try:
-            samples, details = _batch_samples(fn, args, use_graph=True)
+            samples, details = _sample(fn, args, use_graph=True)
         except GraphUnavailable as exc:
             if requested == "graph":
                 raise
             torch.cuda.synchronize()
-            fallback, selected = str(exc), "events"
-            samples, details = _batch_samples(fn, args, use_graph=False)
+            method, fallback = "events", str(exc)
+            samples, details = _sample(fn, args, use_graph=False)
     else:
-        samples, details = _batch_samples(fn, args, use_graph=False)
-    if not samples or any(not math.isfinite(value) or value <= 0 for value in samples):
+        samples, details = _sample(fn, args, use_graph=False)
+    if not samples or not all(math.isfinite(value) and value > 0 for value in samples):
         raise RuntimeError("Invalid device timing; increase the workload/--rep")
-    notice = f"Timing: {selected} via HIP events"
-    if fallback:
-        notice += f" (auto fallback: {fallback}; includes host dispatch gaps)"
+    notice = f"Timing: {method} via HIP events" + (
+        f" (auto fallback: {fallback}; includes host dispatch gaps)" if fallback else "")
     if getattr(args, "_timing_notice", None) != notice:
         print(notice)
         args._timing_notice = notice
     return {
         "median_ms": statistics.median(samples), "p20_ms": _quantile(samples, 0.2),
         "p80_ms": _quantile(samples, 0.8), "min_ms": min(samples), "max_ms": max(samples),
-        "timing_method": selected, "timing_requested": requested,
+        "timing_method": method, "timing_requested": requested,
         "timing_fallback_reason": fallback, "samples_ms_per_launch": samples, **details,
     }
 
