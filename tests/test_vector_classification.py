@@ -109,3 +109,24 @@ def test_wrong_result_is_an_error_before_timing(tmp_path, stand_ins):
         _run(tmp_path)
     assert stand_ins["timed"] == 0
     assert not (tmp_path / "vector.json").exists()
+
+
+def test_bf16_dot2_refuses_operands_outside_its_bounded_regime():
+    """The dot2 form reads the sibling chain times zero, so it runs only where every chain stays finite."""
+    import torch
+
+    from triton_chip_benchmarks_amd import bench_vector, roofline
+
+    inputs = torch.full((8, 64), 0.5, dtype=torch.bfloat16)
+    ok = torch.tensor([-1.0] + [0.125] * 8, dtype=torch.bfloat16)
+    assert bench_vector.dot2_regime_reason(inputs, ok, 4096) is None
+    grows = ok.clone()
+    grows[0] = 1.5
+    assert "|a|" in bench_vector.dot2_regime_reason(inputs, grows, 4096)
+    infinite = inputs.clone()
+    infinite[3, 7] = float("inf")
+    assert "non-finite" in bench_vector.dot2_regime_reason(infinite, ok, 4096)
+    with pytest.raises(ValueError, match="bf16_fma"):
+        bench_vector.launch_vector("bf16_dot2", infinite, infinite.clone(), ok, 16, 16, 64)
+    ceiling, basis = roofline.ISSUED_CEILINGS["vector_bf16"]
+    assert ceiling == pytest.approx(256 * 2.4e9 * 256 / 3 / 1e12) and "1.5" in basis

@@ -159,7 +159,32 @@ def make_inputs(dtype: str, elements: int, device, inputs_kind: str = "reference
     return inputs.to(device), coefficients.to(device)
 
 
+def dot2_regime_reason(inputs, coefficients, iterations: int) -> str | None:
+    """Why the BF16 dot2 chains may not run these operands, or None.
+
+    Each v_dot2_f32_bf16 computes a*x_c + 0*x_sibling + b_c, so a sibling
+    chain that reached Inf or NaN would turn 0*x_sibling into NaN and poison a
+    finite chain. That cannot happen when every state starts finite and
+    |a| <= 1: each state then stays within |x0| + iterations * max|b| of zero.
+    Other operands must use the bf16_fma variant.
+    """
+    torch = _torch()
+    a, b = coefficients[0].float(), coefficients[1:].float()
+    if not bool(torch.isfinite(inputs.float()).all()) or not bool(torch.isfinite(coefficients.float()).all()):
+        return "non-finite states or coefficients"
+    if abs(a.item()) > 1.0:
+        return f"|a| = {abs(a.item()):g} > 1 lets a chain grow without bound"
+    bound = inputs.float().abs().max().item() + iterations * b.abs().max().item()
+    if bound > 1e38:
+        return f"states may reach {bound:.3g}, past the bfloat16 range"
+    return None
+
+
 def launch_vector(kind: str, inputs, output, coefficients, iterations: int, unroll: int, block_threads: int):
+    if kind == "bf16_dot2":
+        reason = dot2_regime_reason(inputs, coefficients, iterations)
+        if reason:
+            raise ValueError(f"BF16 dot2 chains need bounded operands ({reason}); use the bf16_fma variant")
     elements = inputs.shape[1]
     size = inputs.numel() * inputs.element_size()
     _native.call("mb_vector_chains", KINDS[kind], inputs.data_ptr(), output.data_ptr(), coefficients.data_ptr(),

@@ -47,6 +47,10 @@ PEAKS: dict[str, tuple[float, str, str]] = {
 # differs from the datasheet row above.
 ISSUED_CEILINGS: dict[str, tuple[float, str]] = {
     "vector_fp32": (_tera(128), "v_fma_f32: 64 lanes x 2 flop/clk/CU"),
+    # Eight v_dot2_f32_bf16 and four v_cvt_pk_bf16_f32 per eight 2-flop updates:
+    # 1.5 wave64 VALU instructions per update, 256 / 3 flop/clk/CU.
+    "vector_bf16": (_tera(256) / 3, "v_dot2_f32_bf16 + v_cvt_pk_bf16_f32: 1.5 VALU instructions per "
+                                    "2-flop update"),
 }
 
 
