@@ -7,8 +7,8 @@ in HBM. Each row is one configuration of the benchmark specification:
 
   hbm_copy        configs[0]  mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from
                               seed 0) into a second buffer; bit-exact
-  peak_bf16       configs[2]  resident-operand variant: a 256x256x64 BF16 LDS
-                              tile looped 1024 times per workgroup, 2 per CU
+  peak_bf16       configs[2]  resident-operand variant: a 128x128x64 BF16 tile,
+                              2 chains, looped 1024 times per workgroup, 4 per CU
   gemm_bf16       configs[2]  BF16 GEMM 8192^3, A, B ~ N(0,1), B column-major
   gemm_fp16       configs[2]  FP16 GEMM 8192^3, same operands
   gemm_fp8        configs[3]  FP8 E4M3 GEMM 8192^3 over {+-0.5, +-1, +-2}; exact
@@ -21,6 +21,11 @@ in HBM. Each row is one configuration of the benchmark specification:
   peak_fp8_dense  the same kernel on the dense {+-0.5, +-1, +-2} set
   peak_mxfp4      17-row table: MXFP4 resident tile 128x128x256, 2 chains,
                               the reference's +-0.5/+-1 codes
+
+The resident tiles issue the 16x16 form of each MFMA (v_mfma_f32_16x16x32_bf16,
+v_mfma_f32_16x16x128_f8f6f4, v_mfma_scale_f32_16x16x128_f8f6f4): at the same
+MFMA busy fraction it sustains a higher engine clock under the power limit
+than the 32x32 form, which moves four times the accumulator bytes per flop.
 
 value = mean of achieved / MI355X published peak, in percent, over the
 HEADLINE rows (hbm_copy, peak_bf16, gemm_bf16, gemm_fp8, gemm_mxfp4: the
@@ -167,14 +172,14 @@ class PeakWorkload(Workload):
     unit, bound = "TFLOP/s", "mfma"
     LABELS = {"bf16": "bf16", "fp8": "fp8_e4m3", "fp4": "mxfp4_e2m1"}
 
-    def __init__(self, torch, compute_units, name, dtype, tile, chains, per_cu, operands="lattice"):
+    def __init__(self, torch, compute_units, name, dtype, tile, chains, per_cu, operands="lattice", mfma_m=32):
         from triton_chip_benchmarks_amd import _native, bench_tensor
 
         self.torch, self.bt, self.dtype, self.name = torch, bench_tensor, dtype, name
         self.row, self.label = f"tensor_{dtype}", self.LABELS[dtype]
         m, n, k = tile
         self.cfg = next(c for c in _native.peak_configs(dtype) if (c["tile_m"], c["tile_n"], c["tile_k"]) == tile
-                        and c["chains"] == chains and not c["b_nk"])
+                        and c["chains"] == chains and c["mfma_m"] == mfma_m and not c["b_nk"])
         self.kernel = _native.peak_kernel_name(dtype, self.cfg)
         self.blocks = per_cu * compute_units
         if dtype == "fp4":
@@ -190,7 +195,8 @@ class PeakWorkload(Workload):
         self.reference = bench_tensor.exact_reference(self.values[0], self.values[1], PEAK_ITERATIONS,
                                                       torch.float32)
         self.work = 2 * m * n * k * PEAK_ITERATIONS * chains * self.blocks  # bench_tensor.py:1242
-        self.config = {"tile": f"{m}x{n}x{k}", "chains": chains, "blocks": self.blocks, "blocks_per_cu": per_cu,
+        self.config = {"tile": f"{m}x{n}x{k}", "mfma": f"{mfma_m}x{mfma_m}", "chains": chains,
+                       "blocks": self.blocks, "blocks_per_cu": per_cu,
                        "iterations": PEAK_ITERATIONS, "b_layout": "kn", "operands": operand_text}
 
     def launch(self):
@@ -261,15 +267,15 @@ class GemmWorkload(Workload):
 
 def _row_specs():
     """(name, factory) in run order; factories take (torch, compute_units)."""
-    def peak(name, dtype, tile, chains, per_cu, operands="lattice"):
-        return name, lambda t, cu: PeakWorkload(t, cu, name, dtype, tile, chains, per_cu, operands)
+    def peak(name, dtype, tile, chains, per_cu, operands="lattice", mfma_m=16):
+        return name, lambda t, cu: PeakWorkload(t, cu, name, dtype, tile, chains, per_cu, operands, mfma_m)
 
     def gemm(name, dtype, size):
         return name, lambda t, cu: GemmWorkload(t, cu, name, dtype, size)
 
     return [
         ("hbm_copy", CopyWorkload),
-        peak("peak_bf16", "bf16", (256, 256, 64), 1, 2),
+        peak("peak_bf16", "bf16", (128, 128, 64), 2, 4),
         gemm("gemm_bf16", "bf16", 8192),
         gemm("gemm_fp16", "fp16", 8192),
         gemm("gemm_fp8", "fp8", 8192),

@@ -24,6 +24,10 @@ PEAK_INSTRUCTION = {"bf16": "v_mfma_f32_32x32x16_bf16", "fp16": "v_mfma_f32_32x3
                     "int8": "v_mfma_i32_32x32x32_i8", "fp8": "v_mfma_f32_32x32x64_f8f6f4",
                     "fp4": "v_mfma_scale_f32_32x32x64_f8f6f4", "fp32": "v_mfma_f32_32x32x2_f32",
                     "fp64": "v_mfma_f64_16x16x4_f64"}
+# The _mfma16 peak tiles issue the 16x16 form of the same instruction.
+PEAK_INSTRUCTION_16 = {"bf16": "v_mfma_f32_16x16x32_bf16", "fp16": "v_mfma_f32_16x16x32_f16",
+                       "int8": "v_mfma_i32_16x16x64_i8", "fp8": "v_mfma_f32_16x16x128_f8f6f4",
+                       "fp4": "v_mfma_scale_f32_16x16x128_f8f6f4"}
 VECTOR_INSTRUCTION = {"f32": ("fp32", "v_fma_f32"), "f64": ("fp64", "v_fma_f64"), "f16": ("fp16", "v_pk_fma_f16"),
                       "bf16dot": ("bf16", "v_dot2_f32_bf16"), "dot4": ("int8", "v_dot4_i32_i8")}
 
@@ -129,10 +133,11 @@ def test_every_peak_kernel_runs_only_its_mfma_in_the_timed_loop(listing):
     assert len(peak) >= 40
     for name in peak:
         fmt = _peak_format(name)
+        expected = (PEAK_INSTRUCTION_16 if "_mfma16_" in name else PEAK_INSTRUCTION)[fmt]
         result = audit.audit_tensor(audit.instructions(name), fmt)
-        assert result["tensor_instruction_types"] == [PEAK_INSTRUCTION[fmt]], name
+        assert result["tensor_instruction_types"] == [expected], name
         summary = audit.loop_summary(name)
-        assert summary["timed_loop_matrix_types"] == [PEAK_INSTRUCTION[fmt]], name
+        assert summary["timed_loop_matrix_types"] == [expected], name
         assert summary["timed_loop_matrix_instructions"] >= 2, name
         # Only scalar loop control and waits beside the MFMAs; FP64 also moves
         # accumulator halves between AGPRs and VGPRs.

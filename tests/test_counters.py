@@ -41,6 +41,9 @@ def test_registered_names_of_demangled_kernels():
         "void mb::(anonymous namespace)::tensor_peak_kernel<mb::MfmaMxfp4, 128, 128, 256, 2, 2, 2, false>"
         "(unsigned char const*)") == "tensor_peak_mxfp4_128x128x256_c2_kn"
     assert counters.registered_name(
+        "void mb::(anonymous namespace)::tensor_peak_kernel<mb::MfmaBf16x16, 128, 128, 64, 2, 2, 2, true>"
+        "(unsigned char const*)") == "tensor_peak_bf16_128x128x64_c2_mfma16_nk"
+    assert counters.registered_name(
         "void mb::(anonymous namespace)::gemm_kernel<mb::MfmaF64, 64, 64, 16, 2, 2, true>(int)") == \
         "gemm_f64_64x64x16_checked"
     assert counters.registered_name("void mb::(anonymous namespace)::vector_dot4_kernel<16>(int const*)") == \

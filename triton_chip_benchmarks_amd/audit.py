@@ -44,7 +44,9 @@ def registered_name(symbol: str) -> str | None:
     match = _PEAK_RE.search(symbol)
     if match:
         op, bm, bn, bk, _wm, _wn, chains, nk = match.groups()
-        return f"tensor_peak_{_MFMA_FORMAT[op]}_{bm}x{bn}x{bk}_c{chains}_{'nk' if nk == '1' else 'kn'}"
+        shape = "_mfma16" if op.endswith("x16") else ""
+        return (f"tensor_peak_{_MFMA_FORMAT[op.removesuffix('x16')]}_{bm}x{bn}x{bk}_c{chains}{shape}_"
+                f"{'nk' if nk == '1' else 'kn'}")
     match = _GEMM_RE.search(symbol)
     if match:
         op, bm, bn, bk, _wm, _wn, checked = match.groups()

@@ -366,7 +366,7 @@ def run_peak(args, metadata: dict, device) -> None:
             "MX FP4 (E2M1) operands with E8M0 group scales" if args.dtype == "fp4" else f"{args.dtype} operands")
     print(f"\nMatrix peak: resident {text}, independent {accumulator.upper()} accumulator chains (v_mfma)")
     print(f"Iterations={args.iterations}; operations=2*tile_M*tile_N*tile_K*iterations*chains*blocks")
-    print(f" tile M/N/K      chains  blocks/CU  median ms    min ms  median {unit}  peak {unit}  % peak  regs")
+    print(f" tile M/N/K     mfma  chains  blocks/CU  median ms    min ms  median {unit}  peak {unit}  % peak  regs")
     rows = []
     for config in candidates:
         m, n, k, chains = config["tile_m"], config["tile_n"], config["tile_k"], config["chains"]
@@ -410,7 +410,8 @@ def run_peak(args, metadata: dict, device) -> None:
                 measurement_kind = "native_tensor_peak" if info["native_tensor_verified"] else "unverified"
             row = {"mode": "peak", "dtype": args.dtype,
                    "config": {"block_m": m, "block_n": n, "block_k": k, "chains": chains,
-                              "b_layout": "nk" if config["b_nk"] else "kn", "threads": config["threads"]},
+                              "b_layout": "nk" if config["b_nk"] else "kn", "threads": config["threads"],
+                              "mfma_m": config["mfma_m"]},
                    "kernel": kernel, "measurement_kind": measurement_kind,
                    "execution_kind": info["execution_kind"],
                    "precision_verified": bool(metadata.get("tensor_precision_probe"))
@@ -428,7 +429,7 @@ def run_peak(args, metadata: dict, device) -> None:
                    "roofline": roofline.describe(f"tensor_{args.dtype}", row_rates["peak_teraops_per_second"]),
                    **timing}
             rows.append(row)
-            print(f"{m:>4}/{n}/{k:<5} {chains:>6} {blocks_per_sm:10d} {timing['median_ms']:10.4f} "
+            print(f"{m:>4}/{n}/{k:<5} {config['mfma_m']:>2}x{config['mfma_m']:<2} {chains:>6} {blocks_per_sm:10d} {timing['median_ms']:10.4f} "
                   f"{timing['min_ms']:9.4f} {row_rates['median_teraops_per_second']:12.2f} "
                   f"{row_rates['peak_teraops_per_second']:10.2f} "
                   f"{100 * row_rates['peak_teraops_per_second'] / peak_value:7.1f} "

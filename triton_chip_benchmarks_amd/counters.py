@@ -101,7 +101,9 @@ def registered_name(demangled: str) -> str:
     family, args = parsed[0], [part.replace("mb::", "") for part in parsed[1]]
     if family == "tensor_peak_kernel":
         fmt, bm, bn, bk, _wm, _wn, chains, nk = args
-        return f"tensor_peak_{_MFMA_FORMAT[fmt]}_{bm}x{bn}x{bk}_c{chains}_{'nk' if nk in ('true', '1') else 'kn'}"
+        shape = "_mfma16" if fmt.endswith("x16") else ""
+        return (f"tensor_peak_{_MFMA_FORMAT[fmt.removesuffix('x16')]}_{bm}x{bn}x{bk}_c{chains}{shape}_"
+                f"{'nk' if nk in ('true', '1') else 'kn'}")
     if family == "gemm_kernel":
         fmt, bm, bn, bk, _wm, _wn, checked = args
         return f"gemm_{_MFMA_FORMAT[fmt]}_{bm}x{bn}x{bk}{'_checked' if checked in ('true', '1') else ''}"
@@ -325,7 +327,8 @@ def target(report_path: Path, launches: int, selected=None) -> None:
             peak = next(c for c in _native.peak_configs(dtype)
                         if (c["tile_m"], c["tile_n"], c["tile_k"], c["chains"]) ==
                         (tile["block_m"], tile["block_n"], tile["block_k"], tile["chains"])
-                        and bool(c["b_nk"]) == (tile.get("b_layout") == "nk"))
+                        and bool(c["b_nk"]) == (tile.get("b_layout") == "nk")
+                        and c["mfma_m"] == tile.get("mfma_m", 32))
             if dtype == "fp4":
                 a, b, c, scales, _values = bench_tensor.fp4_peak_inputs(config["blocks"], peak, "cuda")
             else:

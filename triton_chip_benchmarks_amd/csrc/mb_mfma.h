@@ -115,6 +115,75 @@ struct MfmaMxfp4 {
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
 };
 
+// 16x16 forms of the same instructions. Per flop they move a quarter of the
+// accumulator bytes of the 32x32 forms and twice the operand bytes; the
+// resident-peak tables carry both so the sweep measures which one the power
+// limit favours. Lane groups are 64 / 16 = 4, so a lane's K slice is a quarter
+// of the instruction's K.
+struct MfmaBf16x16 {
+  static constexpr int M = 16, N = 16, K = 32, ELEM_BITS = 16, LANE_BYTES = 16, ACC_REGS = 4;
+  static constexpr bool SCALED = false;
+  using Frag = i32x4;
+  using Acc = f32x4;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
+};
+
+struct MfmaF16x16 {
+  static constexpr int M = 16, N = 16, K = 32, ELEM_BITS = 16, LANE_BYTES = 16, ACC_REGS = 4;
+  static constexpr bool SCALED = false;
+  using Frag = i32x4;
+  using Acc = f32x4;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
+};
+
+struct MfmaI8x16 {
+  static constexpr int M = 16, N = 16, K = 64, ELEM_BITS = 8, LANE_BYTES = 16, ACC_REGS = 4;
+  static constexpr bool SCALED = false;
+  using Frag = i32x4;
+  using Acc = i32x4;
+  using Out = int32_t;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
+};
+
+struct MfmaFp8x16 {
+  static constexpr int M = 16, N = 16, K = 128, ELEM_BITS = 8, LANE_BYTES = 32, ACC_REGS = 4;
+  static constexpr bool SCALED = false;
+  using Frag = i32x8;
+  using Acc = f32x4;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
+};
+
+struct MfmaMxfp4x16 {
+  static constexpr int M = 16, N = 16, K = 128, ELEM_BITS = 4, LANE_BYTES = 16, ACC_REGS = 4;
+  static constexpr bool SCALED = true;
+  using Frag = i32x4;
+  using Acc = f32x4;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int scale_a, int scale_b) {
+    const i32x8 wa = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+    const i32x8 wb = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wa, wb, c, 4, 4, 0, scale_a, 0, scale_b);
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
+};
+
 // v_mfma_f32_32x32x2_f32: one fp32 per lane, IEEE fp32 multiply-accumulate.
 struct MfmaF32 {
   static constexpr int M = 32, N = 32, K = 2, ELEM_BITS = 32, LANE_BYTES = 4, ACC_REGS = 16;
