@@ -27,10 +27,12 @@ def _write_pass(directory, records):
     with (directory / "run_counter_collection.csv").open("w", newline="") as stream:
         writer = csv.DictWriter(stream, FIELDS)
         writer.writeheader()
-        for dispatch, kernel, counter, value, duration_ns in records:
+        for dispatch, kernel, counter, value, duration_ns, *grid in records:
             row = dict.fromkeys(FIELDS, 0)
             row.update(Dispatch_Id=dispatch, Kernel_Name=kernel, Counter_Name=counter, Counter_Value=value,
                        Start_Timestamp=1000, End_Timestamp=1000 + duration_ns)
+            if grid:
+                row.update(Grid_Size=grid[0], Workgroup_Size=grid[1])
             writer.writerow(row)
 
 
@@ -109,3 +111,23 @@ def test_every_pass_fits_one_rocprofv3_run():
     command = counters.rocprof_command(["SQ_WAVE_CYCLES"], "/tmp/x", ["python3", "prog.py"])
     assert command[command.index("--") + 1:] == ["python3", "prog.py"]
     assert not {"--sys-trace", "-s", "--runtime-trace", "-r"} & set(command)
+
+
+def test_by_grid_keeps_workgroup_counts_apart(tmp_path):
+    """A sweep of workgroups per CU launches one kernel over several grids."""
+    peak = ("void mb::(anonymous namespace)::tensor_peak_kernel<mb::MfmaBf16x16, 128, 128, 64, 2, 2, 2, false>"
+            "(unsigned char const*)")
+    records = []
+    for dispatch, (blocks, ghz) in enumerate([(256, 2.0), (256, 2.0), (1024, 2.2)], start=1):
+        cycles = ghz * 1e6  # per XCD over a 1 ms launch
+        records += [(dispatch, peak, "GRBM_GUI_ACTIVE", cycles * counters.XCDS, 1_000_000, 256 * blocks, 256),
+                    (dispatch, peak, "SQ_VALU_MFMA_BUSY_CYCLES", 0.9 * cycles * counters.SIMDS, 1_000_000,
+                     256 * blocks, 256)]
+    _write_pass(tmp_path / "sq", records)
+    merged = counters.summarize(tmp_path)["kernels"]
+    assert list(merged) == ["tensor_peak_bf16_128x128x64_c2_mfma16_kn"]
+    assert merged["tensor_peak_bf16_128x128x64_c2_mfma16_kn"]["clock_ghz"] == pytest.approx(2.0667, rel=1e-3)
+    apart = counters.summarize(tmp_path, by_grid=True)["kernels"]
+    assert apart["tensor_peak_bf16_128x128x64_c2_mfma16_kn@256wg"]["clock_ghz"] == pytest.approx(2.0)
+    assert apart["tensor_peak_bf16_128x128x64_c2_mfma16_kn@1024wg"]["clock_ghz"] == pytest.approx(2.2)
+    assert apart["tensor_peak_bf16_128x128x64_c2_mfma16_kn@1024wg"]["mfma_busy"] == pytest.approx(0.9)

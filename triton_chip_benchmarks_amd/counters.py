@@ -164,8 +164,12 @@ def _complete(directory: Path) -> bool:
 
 # ---- summarize ---------------------------------------------------------------
 
-def load_pass(directory: Path) -> dict[str, dict[int, dict]]:
-    """kernel -> dispatch id -> {counter: value, 'duration_ns': ns} for one pass."""
+def load_pass(directory: Path, by_grid: bool = False) -> dict[str, dict[int, dict]]:
+    """kernel -> dispatch id -> {counter: value, 'duration_ns': ns} for one pass.
+
+    With by_grid, launches of one kernel over different grids are kept apart
+    under `kernel@<workgroups>wg` (a sweep of workgroups per CU, for example).
+    """
     path = _counter_csv(directory)
     if path is None:
         return {}
@@ -173,6 +177,8 @@ def load_pass(directory: Path) -> dict[str, dict[int, dict]]:
     with path.open() as stream:
         for record in csv.DictReader(stream):
             name = registered_name(record["Kernel_Name"])
+            if by_grid:
+                name += f"@{int(record['Grid_Size']) // max(1, int(record['Workgroup_Size']))}wg"
             dispatch = kernels.setdefault(name, {}).setdefault(int(record["Dispatch_Id"]), {})
             dispatch[record["Counter_Name"]] = dispatch.get(record["Counter_Name"], 0.0) + float(
                 record["Counter_Value"])
@@ -195,11 +201,12 @@ def _per_dispatch(dispatches, formula):
     return _mean(out)
 
 
-def summarize(out: Path) -> dict:
-    passes = {name: load_pass(out / name) for name in PASSES if (out / name).exists()}
+def summarize(out: Path, by_grid: bool = False) -> dict:
+    passes = {name: load_pass(out / name, by_grid) for name in PASSES if (out / name).exists()}
     kernels = sorted({kernel for data in passes.values() for kernel in data})
     fetch, write = passes.get("fetch", {}), passes.get("write", {})
-    calibration = next((k for k in CALIBRATION_KERNELS if k in fetch and k in write), None)
+    calibration = next((k for base in CALIBRATION_KERNELS for k in fetch
+                        if k.split("@")[0] == base and k in write), None)
     f_read = f_write = None
     if calibration:
         f_read = _per_dispatch(fetch[calibration], lambda v: v["FETCH_SIZE"] * 1024) / CALIBRATION_BYTES
@@ -367,6 +374,8 @@ def main(argv=None) -> int:
     p.add_argument("--out", type=Path, required=True)
     p.add_argument("--json", type=Path)
     p.add_argument("--markdown", type=Path)
+    p.add_argument("--by-grid", action="store_true",
+                   help="keep launches of one kernel over different grids apart (kernel@<workgroups>wg)")
     p = sub.add_parser("attach", help="copy kernel summaries into a report's rows")
     p.add_argument("--summary", type=Path, required=True)
     p.add_argument("--report", type=Path, required=True)
@@ -379,7 +388,7 @@ def main(argv=None) -> int:
     elif args.command == "target":
         target(args.report, args.launches, args.rows)
     elif args.command == "summarize":
-        summary = summarize(args.out)
+        summary = summarize(args.out, args.by_grid)
         if args.json:
             args.json.write_text(json.dumps(summary, indent=2) + "\n")
         text = markdown(summary)
