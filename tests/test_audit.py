@@ -150,8 +150,11 @@ def test_every_gemm_kernel_uses_its_format_mfma(listing):
     assert gemm
     for name in gemm:
         fmt = FORMAT_OF[name.split("_")[1]]
+        # The staged 256x256 BF16/FP16/INT8 kernels issue the 16x16 form.
+        staged16 = fmt in ("bf16", "fp16", "int8") and "_256x256x" in name and not name.endswith("_checked")
+        expected = (PEAK_INSTRUCTION_16 if staged16 else PEAK_INSTRUCTION)[fmt]
         result = audit.audit_tensor(audit.instructions(name), fmt)
-        assert result["tensor_instruction_types"] == [PEAK_INSTRUCTION[fmt]], name
+        assert result["tensor_instruction_types"] == [expected], name
 
 
 def test_every_vector_kernel_issues_its_native_instruction_and_no_mfma(listing):
@@ -197,3 +200,21 @@ def test_copy_policies_issue_their_cache_bits(listing):
 def test_no_packed_fp32_valu_anywhere():
     text = native_build.DISASSEMBLY.read_text()
     assert not re.search(r"\bv_pk_(?:add|mul|fma|mov)_f32\b", text)
+
+
+@pytest.mark.parametrize("name,instruction", [("gemm_bf16_256x256x64", "v_mfma_f32_16x16x32_bf16"),
+                                              ("gemm_f16_256x256x64", "v_mfma_f32_16x16x32_f16"),
+                                              ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8")])
+def test_staged_16x16_gemm_loop_has_no_accumulator_copies(listing, name, instruction):
+    """The in-place 16x16 MFMAs keep every accumulator in its AGPRs: the K loop
+    (two 128-byte steps) issues 256 MFMAs, 64 fragment reads, 32 stage writes,
+    32 loads and nothing else on the vector side, with no spills."""
+    assert name in listing
+    resources = audit.resources(name)
+    assert resources["register_spills"] == 0 and resources["scratch_bytes"] == 0
+    summary = audit.loop_summary(name)
+    assert summary["timed_loop_matrix_types"] == [instruction]
+    assert summary["timed_loop_matrix_instructions"] == 256
+    assert summary["timed_loop_vector_memory_or_alu"] == {"ds_read_b128": 64, "ds_write_b128": 32,
+                                                          "buffer_load_dwordx4": 32}
+    assert summary["timed_loop_other_instructions"]["s_barrier"] == 2

@@ -58,7 +58,7 @@ def registered_name(symbol: str) -> str | None:
         return f"gemm_{fmt}_256x256x{int(row_bytes) * 8 // _ELEM_BITS[fmt]}"
     match = _GEMM_STAGED_RE.search(symbol)
     if match:
-        fmt = _MFMA_FORMAT[match.group(1)]
+        fmt = _MFMA_FORMAT[match.group(1).removesuffix("x16")]
         return f"gemm_{fmt}_256x256x{128 * 8 // _ELEM_BITS[fmt]}"
     match = _COPY_RE.search(symbol)
     if match:

@@ -112,7 +112,7 @@ def registered_name(demangled: str) -> str:
         name = _MFMA_FORMAT[fmt]
         return f"gemm_{name}_256x256x{row_bytes * 8 // _ELEM_BITS[name]}"
     if family == "gemm_staged_kernel":
-        name = _MFMA_FORMAT[args[0]]
+        name = _MFMA_FORMAT[args[0].removesuffix("x16")]
         return f"gemm_{name}_256x256x{128 * 8 // _ELEM_BITS[name]}"
     if family == "copy_kernel":
         unit = "dwordx4" if "__vector(4)" in args[0] else "byte" if "char" in args[0] else "dword"

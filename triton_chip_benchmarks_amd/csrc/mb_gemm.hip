@@ -15,7 +15,9 @@
 // Two kernels:
 //   * gemm_staged_kernel: 256x256 tiles of BF16, FP16, INT8, FP8 and MXFP4
 //     when the shape divides the tile. Four waves, one per SIMD, each owning
-//     128x128 outputs (16 accumulators of 32x32 in AGPRs). Operands flow
+//     128x128 outputs in AGPRs: 64 accumulators of 16x16 for BF16, FP16 and
+//     INT8 (the 16x16 instructions sustain a higher clock under the power
+//     limit), 16 of 32x32 for FP8 and MXFP4. Operands flow
 //     global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128 bytes of every
 //     row) is loaded two steps ahead into one of two register sets, written to
 //     one of two LDS stages a step ahead, and read back as fragments ahead of
@@ -292,8 +294,11 @@ __global__ void __launch_bounds__(256)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NL = 16;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
   constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = Op::SCALED ? 4 : 0;
-  static_assert(Op::M == 32 && ((PIECES == 1 && KS == 4) || (PIECES == 2 && KS == 2 && !Op::SCALED)),
-                "16-byte fragments in four substeps, or unscaled 32-byte fragments in two");
+  static_assert((Op::M == 32 && ((PIECES == 1 && KS == 4) || (PIECES == 2 && KS == 2 && !Op::SCALED))) ||
+                    (Op::M == 16 && PIECES == 1 && KS == 2 && !Op::SCALED),
+                "32x32: 16-byte fragments in four substeps, or unscaled 32-byte fragments in two; "
+                "16x16: unscaled 16-byte fragments in two substeps");
+  constexpr int TILES = 128 / Op::M;  // fragments per wave side (4 for 32x32, 8 for 16x16)
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * REGION + SCALE_RING * SCALE_STAGE];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written (scale) reads live; never executed
 
@@ -381,11 +386,11 @@ __global__ void __launch_bounds__(256)
     }
   };
 
-  typename Op::Acc acc[4][4];
+  typename Op::Acc acc[TILES][TILES];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = typename Op::Acc{};
+    for (int j = 0; j < TILES; ++j) acc[i][j] = typename Op::Acc{};
 
   i32x4 v0[NL], v1[NL];
   // Prologue: steps 0 and 1 in flight, step 0 into stage 0, step 2 into v0.
@@ -399,7 +404,81 @@ __global__ void __launch_bounds__(256)
   load(v0, 2, 0, NL);
   lds_barrier();
 
-  if constexpr (PIECES == 1) {
+  if constexpr (Op::M == 16) {
+    // 16x16 instructions: eight A and eight B fragments (16 rows each) per
+    // substep, held in one set each and refilled as their last MFMA issues.
+    // Rows 0..5 run one row at a time, A_i refilled after its row; rows 6 and 7
+    // run interleaved by column, B_j refilled after (7, j), then A_6 and A_7;
+    // B_7, the last refill, has the next substep's first seven MFMAs to land.
+    // The MFMAs are the in-place (tied) forms, so program order is the issue
+    // order: every MFMA is its own scheduling region, and the memory work of
+    // rows 0..5 is dealt out over their 48 slots: stage writes (substep 0) in
+    // every third slot, each load behind the write that frees its registers.
+    // The in-place forms' hazard fences sit around the loop.
+    const int lrow16 = lane & 15, lgroup16 = lane >> 4;
+    const int sw16 = ((lrow16 >> 1) & 7) ^ lgroup16;
+    const uint32_t ra16 = (wm * 128 + lrow16) * ROWB + (sw16 << 4);
+    const uint32_t rb16 = 2 * REGION + (wn * 128 + lrow16) * ROWB + (sw16 << 4);
+    // Fragment f of substep ks: its row's logical chunk ks*4 + lane group, so
+    // the lane base XOR (ks*4 << 4); fragments are 16 rows (2 KiB) apart.
+    auto frag = [&](uint32_t off, int s, int ks, int f) __attribute__((always_inline)) {
+      return *reinterpret_cast<const i32x4*>(lds + (off ^ (static_cast<uint32_t>(ks) << 6)) + s * REGION +
+                                             f * 16 * ROWB);
+    };
+    i32x4 fa[8], fb[8];
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      fa[f] = frag(ra16, 0, 0, f);
+      fb[f] = frag(rb16, 0, 0, f);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
+    auto step = [&](int kt, int s, i32x4 (&vnext)[NL]) __attribute__((always_inline)) {
+      static_for<0, KS>([&](auto ks_c) __attribute__((always_inline)) {
+        constexpr int ks = decltype(ks_c)::value;
+        const int ns = ks + 1 < KS ? s : s ^ 1, nks = ks + 1 < KS ? ks + 1 : 0;
+        auto mma = [&](int i, int j) __attribute__((always_inline)) { Op::mma_tied(fa[i], fb[j], acc[i][j]); };
+        static_for<0, 48>([&](auto slot_c) __attribute__((always_inline)) {
+          constexpr int slot = decltype(slot_c)::value, i = slot / 8, j = slot % 8;
+          if constexpr (ks == 0 && slot % 3 == 0) store(vnext, s ^ 1, slot / 3, slot / 3 + 1);
+          if constexpr (slot % 6 == 1) {
+            constexpr int l = ks * NL / KS + slot / 6;
+            load(vnext, min(kt + 3, last), l, l + 1);
+          }
+          mma(i, j);
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (j == 7) {
+            fa[i] = frag(ra16, ns, nks, i);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        });
+        static_for<0, 8>([&](auto j_c) __attribute__((always_inline)) {
+          constexpr int j = decltype(j_c)::value;
+          mma(6, j);
+          __builtin_amdgcn_sched_barrier(0);
+          mma(7, j);
+          __builtin_amdgcn_sched_barrier(0);
+          fb[j] = frag(rb16, ns, nks, j);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        fa[6] = frag(ra16, ns, nks, 6);
+        fa[7] = frag(ra16, ns, nks, 7);
+        if constexpr (ks == KS - 2) lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
+    for (int kt = 0; kt < k_steps; kt += 2) {
+      step(kt, 0, v1);
+      step(kt + 1, 1, v0);
+    }
+    // Fences in the order of the last substep's writes: rows 0..5, then 6 and 7.
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
+  } else if constexpr (PIECES == 1) {
     // 16-byte fragments: A and B fragments of a substep double-buffered (fa/fb).
     Frag8 fa, fb;
     Scales8 sa0, sa1;
@@ -524,13 +603,13 @@ __global__ void __launch_bounds__(256)
   }
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < TILES; ++j)
 #pragma unroll
       for (int r = 0; r < Op::ACC_REGS; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + Op::out_row(lane, r);
-        const int col = n0 + wn * 128 + j * 32 + lrow;
+        const int row = m0 + wm * 128 + i * Op::M + Op::out_row(lane, r);
+        const int col = n0 + wn * 128 + j * Op::N + lane % Op::N;
         C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
       }
 #endif
@@ -590,14 +669,15 @@ struct GemmVariant {
               NAME "_checked",                                                                               \
               reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, true>)}
 
-// 256x256 tiles: the staged kernel (BK = 128 bytes of K) for exact shapes, a
-// checked LDS-staged kernel (tile CM x CN) for the rest.
-#define MB_GEMM_STAGED(FMT, OP, BK, CM, CN, NAME, CNAME)                                                          \
+// 256x256 tiles: the staged kernel (BK = 128 bytes of K; instruction SOP) for
+// exact shapes, a checked LDS-staged kernel (tile CM x CN, instruction OP) for
+// the rest.
+#define MB_GEMM_STAGED(FMT, SOP, OP, BK, CM, CN, NAME, CNAME)                                                     \
   GemmVariant{FMT,                                                                                           \
               mb_gemm_config{256, 256, BK, 256},                                                             \
               NAME,                                                                                          \
-              reinterpret_cast<const void*>(gemm_staged_kernel<OP>),                                         \
-              launch_gemm_staged<OP>,                                                                        \
+              reinterpret_cast<const void*>(gemm_staged_kernel<SOP>),                                        \
+              launch_gemm_staged<SOP>,                                                                       \
               launch_gemm<OP, CM, CN, BK, 2, 2, true>,                                                       \
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
               OP::ELEM_BITS,                                                                                 \
@@ -605,23 +685,23 @@ struct GemmVariant {
               CNAME,                                                                               \
               reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>)}
 const GemmVariant kGemmVariants[] = {
-    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64",
+    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16x16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64",
                    "gemm_bf16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
-    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16, 64, 256, 256, "gemm_f16_256x256x64",
+    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16x16, MfmaF16, 64, 256, 256, "gemm_f16_256x256x64",
                    "gemm_f16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128",
+    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128",
                    "gemm_fp8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
-    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128",
+    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8x16, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128",
                    "gemm_i8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
-    MB_GEMM_STAGED(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 128, "gemm_mxfp4_256x256x256",
+    MB_GEMM_STAGED(MB_MATRIX_MXFP4, MfmaMxfp4, MfmaMxfp4, 256, 128, 128, "gemm_mxfp4_256x256x256",
                    "gemm_mxfp4_128x128x256_checked"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, "gemm_mxfp4_128x128x256"),

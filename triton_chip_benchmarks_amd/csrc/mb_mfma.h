@@ -120,6 +120,16 @@ struct MfmaMxfp4 {
 // resident-peak tables carry both so the sweep measures which one the power
 // limit favours. Lane groups are 64 / 16 = 4, so a lane's K slice is a quarter
 // of the instruction's K.
+//
+// mma_tied accumulates in place in AGPRs through inline assembly: for the
+// 16x16 forms with 16-byte operands (BF16, FP16, INT8, and FP4 as well)
+// the compiler does not tie the accumulator input to the output, so a loop of
+// them copies every accumulator per instruction (and at 256 accumulator
+// registers spills). The compiler does not see these as MFMAs, so callers keep
+// the hazard distances themselves: operands come straight from LDS loads
+// (whose waits the compiler inserts for any reader), and acc_hazard_fence()
+// separates the accumulators' VALU initialisation from the first MFMA and the
+// last MFMA from the reads that follow.
 struct MfmaBf16x16 {
   static constexpr int M = 16, N = 16, K = 32, ELEM_BITS = 16, LANE_BYTES = 16, ACC_REGS = 4;
   static constexpr bool SCALED = false;
@@ -129,6 +139,9 @@ struct MfmaBf16x16 {
   __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                    c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ void mma_tied(Frag a, Frag b, Acc& c) {
+    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
   }
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
 };
@@ -143,6 +156,9 @@ struct MfmaF16x16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
                                                   0, 0, 0);
   }
+  __device__ static __forceinline__ void mma_tied(Frag a, Frag b, Acc& c) {
+    asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
 };
 
@@ -154,6 +170,9 @@ struct MfmaI8x16 {
   using Out = int32_t;
   __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ void mma_tied(Frag a, Frag b, Acc& c) {
+    asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
   }
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
 };
@@ -211,6 +230,16 @@ struct MfmaF64 {
   // with a row/column-marked product), unlike the 16x16 fp32 forms.
   __device__ static __forceinline__ int out_row(int lane, int r) { return (lane >> 4) + 4 * r; }
 };
+
+// An ordered (volatile) no-op that takes acc as an in-place AGPR operand:
+// called once per accumulator, in the order of their last writes, after the
+// accumulator loop (and after initialisation), so that every accumulator is
+// read only behind at least (number of fences issued before its own) wait
+// states since the loop's last MFMA.
+template <class Acc>
+__device__ __forceinline__ void acc_hazard_fence(Acc& c) {
+  asm volatile("s_nop 1" : "+a"(c));
+}
 
 template <class Op>
 struct MfmaGeometry {
