@@ -51,6 +51,9 @@ def test_registered_names_of_demangled_kernels():
     assert counters.registered_name("void mb::(anonymous namespace)::vector_dot4_kernel<16>(int const*)") == \
         "vector_dot4_u16"
     assert counters.registered_name("Cijk_Alik_Bljk_BBS_BH(int)") == "Cijk_Alik_Bljk_BBS_BH"
+    # A name the profiler left mangled maps through the symbol parser.
+    assert counters.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi16EEEvPKDF16_PDF16_S3_mj") == \
+        "vector_f16_u16"
 
 
 def test_summary_formulas_and_copy_calibration(tmp_path):

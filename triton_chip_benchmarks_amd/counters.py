@@ -95,6 +95,12 @@ def registered_name(demangled: str) -> str:
 
     Kernels outside the library keep a shortened form of their own name.
     """
+    if demangled.startswith("_Z"):  # left mangled by the profiler (e.g. _Float16 arguments)
+        from .audit import registered_name as from_symbol
+
+        name = from_symbol(demangled)
+        if name:
+            return name
     parsed = _template(demangled) if "mb::" in demangled else None
     if parsed is None:
         return re.sub(r"\(.*$", "", demangled.replace("void ", ""))[:120]
