@@ -207,14 +207,18 @@ def test_no_packed_fp32_valu_anywhere():
                                               ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8")])
 def test_staged_16x16_gemm_loop_has_no_accumulator_copies(listing, name, instruction):
     """The in-place 16x16 MFMAs keep every accumulator in its AGPRs: the K loop
-    (two 128-byte steps) issues 256 MFMAs, 64 fragment reads, 32 stage writes,
-    32 loads and nothing else on the vector side, with no spills."""
+    (two 128-byte steps) issues 256 MFMAs, 64 fragment reads, 16 B stage
+    writes and 32 buffer loads (16 of B into registers, 16 LDS-DMA of A) and
+    nothing else on the vector side, with no spills."""
     assert name in listing
     resources = audit.resources(name)
     assert resources["register_spills"] == 0 and resources["scratch_bytes"] == 0
     summary = audit.loop_summary(name)
     assert summary["timed_loop_matrix_types"] == [instruction]
     assert summary["timed_loop_matrix_instructions"] == 256
-    assert summary["timed_loop_vector_memory_or_alu"] == {"ds_read_b128": 64, "ds_write_b128": 32,
-                                                          "buffer_load_dwordx4": 32}
+    vector = dict(summary["timed_loop_vector_memory_or_alu"])
+    assert {k: vector.pop(k, 0) for k in ("ds_read_b128", "ds_write_b128", "buffer_load_dwordx4")} == \
+        {"ds_read_b128": 64, "ds_write_b128": 16, "buffer_load_dwordx4": 32}
+    # What remains is the per-step A slot address (the ring of three slots is not a power of two).
+    assert set(vector) <= {"v_or_b32_e32", "v_lshl_or_b32", "v_add_u32_e32"} and sum(vector.values()) <= 8, vector
     assert summary["timed_loop_other_instructions"]["s_barrier"] == 2

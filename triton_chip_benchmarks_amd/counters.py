@@ -117,7 +117,7 @@ def registered_name(demangled: str) -> str:
         fmt, row_bytes = args[0], int(args[1])
         name = _MFMA_FORMAT[fmt]
         return f"gemm_{name}_256x256x{row_bytes * 8 // _ELEM_BITS[name]}"
-    if family == "gemm_staged_kernel":
+    if family in ("gemm_staged_kernel", "gemm_dma16_kernel"):
         name = _MFMA_FORMAT[args[0].removesuffix("x16")]
         return f"gemm_{name}_256x256x{128 * 8 // _ELEM_BITS[name]}"
     if family == "copy_kernel":

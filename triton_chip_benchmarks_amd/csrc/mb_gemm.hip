@@ -13,17 +13,18 @@
 // timing by the caller).
 //
 // Two kernels:
-//   * gemm_staged_kernel: 256x256 tiles of BF16, FP16, INT8, FP8 and MXFP4
-//     when the shape divides the tile. Four waves, one per SIMD, each owning
-//     128x128 outputs in AGPRs: 64 accumulators of 16x16 for BF16, FP16 and
-//     INT8 (the 16x16 instructions sustain a higher clock under the power
-//     limit), 16 of 32x32 for FP8 and MXFP4. Operands flow
+//   * gemm_dma16_kernel (BF16, FP16, INT8) and gemm_staged_kernel (FP8,
+//     MXFP4): 256x256 tiles when the shape divides the tile. Four waves, one
+//     per SIMD, each owning 128x128 outputs in AGPRs: 64 accumulators of
+//     16x16 (the 16x16 instructions sustain a higher clock under the power
+//     limit) or 16 of 32x32. In the staged kernel operands flow
 //     global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128 bytes of every
 //     row) is loaded two steps ahead into one of two register sets, written to
 //     one of two LDS stages a step ahead, and read back as fragments ahead of
 //     the MFMAs that use them. Loads, stage writes and fragment reads are
 //     spread across the step's MFMAs, so no burst of memory instructions
-//     stalls the in-order MFMA issue; one barrier per step.
+//     stalls the in-order MFMA issue; one barrier per step. The DMA kernel
+//     moves A straight into LDS with LDS-DMA loads instead.
 //   * gemm_kernel: every other tile and every ragged shape (CHECKED
 //     instantiations bound each load and store), operands staged through a
 //     padded, double-buffered LDS tile with 16-byte loads.
@@ -264,7 +265,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// ---- VGPR-staged 256x256 kernel (BF16, FP16, INT8, FP8, MXFP4) --------------
+// ---- VGPR-staged 256x256 kernel (FP8, MXFP4) -------------------------------
 
 // C = A . B^T for M, N multiples of 256, K * bits a multiple of 1024 (128-byte
 // K steps) with an even number of at least 4 steps; A, B byte offsets and the
@@ -294,11 +295,9 @@ __global__ void __launch_bounds__(256)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NL = 16;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
   constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = Op::SCALED ? 4 : 0;
-  static_assert((Op::M == 32 && ((PIECES == 1 && KS == 4) || (PIECES == 2 && KS == 2 && !Op::SCALED))) ||
-                    (Op::M == 16 && PIECES == 1 && KS == 2 && !Op::SCALED),
-                "32x32: 16-byte fragments in four substeps, or unscaled 32-byte fragments in two; "
-                "16x16: unscaled 16-byte fragments in two substeps");
-  constexpr int TILES = 128 / Op::M;  // fragments per wave side (4 for 32x32, 8 for 16x16)
+  static_assert(Op::M == 32 && ((PIECES == 1 && KS == 4) || (PIECES == 2 && KS == 2 && !Op::SCALED)),
+                "16-byte fragments in four substeps, or unscaled 32-byte fragments in two");
+  constexpr int TILES = 4;  // 32x32 fragments per wave side
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * REGION + SCALE_RING * SCALE_STAGE];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written (scale) reads live; never executed
 
@@ -404,81 +403,7 @@ __global__ void __launch_bounds__(256)
   load(v0, 2, 0, NL);
   lds_barrier();
 
-  if constexpr (Op::M == 16) {
-    // 16x16 instructions: eight A and eight B fragments (16 rows each) per
-    // substep, held in one set each and refilled as their last MFMA issues.
-    // Rows 0..5 run one row at a time, A_i refilled after its row; rows 6 and 7
-    // run interleaved by column, B_j refilled after (7, j), then A_6 and A_7;
-    // B_7, the last refill, has the next substep's first seven MFMAs to land.
-    // The MFMAs are the in-place (tied) forms, so program order is the issue
-    // order: every MFMA is its own scheduling region, and the memory work of
-    // rows 0..5 is dealt out over their 48 slots: stage writes (substep 0) in
-    // every third slot, each load behind the write that frees its registers.
-    // The in-place forms' hazard fences sit around the loop.
-    const int lrow16 = lane & 15, lgroup16 = lane >> 4;
-    const int sw16 = ((lrow16 >> 1) & 7) ^ lgroup16;
-    const uint32_t ra16 = (wm * 128 + lrow16) * ROWB + (sw16 << 4);
-    const uint32_t rb16 = 2 * REGION + (wn * 128 + lrow16) * ROWB + (sw16 << 4);
-    // Fragment f of substep ks: its row's logical chunk ks*4 + lane group, so
-    // the lane base XOR (ks*4 << 4); fragments are 16 rows (2 KiB) apart.
-    auto frag = [&](uint32_t off, int s, int ks, int f) __attribute__((always_inline)) {
-      return *reinterpret_cast<const i32x4*>(lds + (off ^ (static_cast<uint32_t>(ks) << 6)) + s * REGION +
-                                             f * 16 * ROWB);
-    };
-    i32x4 fa[8], fb[8];
-#pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      fa[f] = frag(ra16, 0, 0, f);
-      fb[f] = frag(rb16, 0, 0, f);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
-    auto step = [&](int kt, int s, i32x4 (&vnext)[NL]) __attribute__((always_inline)) {
-      static_for<0, KS>([&](auto ks_c) __attribute__((always_inline)) {
-        constexpr int ks = decltype(ks_c)::value;
-        const int ns = ks + 1 < KS ? s : s ^ 1, nks = ks + 1 < KS ? ks + 1 : 0;
-        auto mma = [&](int i, int j) __attribute__((always_inline)) { Op::mma_tied(fa[i], fb[j], acc[i][j]); };
-        static_for<0, 48>([&](auto slot_c) __attribute__((always_inline)) {
-          constexpr int slot = decltype(slot_c)::value, i = slot / 8, j = slot % 8;
-          if constexpr (ks == 0 && slot % 3 == 0) store(vnext, s ^ 1, slot / 3, slot / 3 + 1);
-          if constexpr (slot % 6 == 1) {
-            constexpr int l = ks * NL / KS + slot / 6;
-            load(vnext, min(kt + 3, last), l, l + 1);
-          }
-          mma(i, j);
-          __builtin_amdgcn_sched_barrier(0);
-          if constexpr (j == 7) {
-            fa[i] = frag(ra16, ns, nks, i);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-        });
-        static_for<0, 8>([&](auto j_c) __attribute__((always_inline)) {
-          constexpr int j = decltype(j_c)::value;
-          mma(6, j);
-          __builtin_amdgcn_sched_barrier(0);
-          mma(7, j);
-          __builtin_amdgcn_sched_barrier(0);
-          fb[j] = frag(rb16, ns, nks, j);
-          __builtin_amdgcn_sched_barrier(0);
-        });
-        fa[6] = frag(ra16, ns, nks, 6);
-        fa[7] = frag(ra16, ns, nks, 7);
-        if constexpr (ks == KS - 2) lds_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    };
-    for (int kt = 0; kt < k_steps; kt += 2) {
-      step(kt, 0, v1);
-      step(kt + 1, 1, v0);
-    }
-    // Fences in the order of the last substep's writes: rows 0..5, then 6 and 7.
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
-  } else if constexpr (PIECES == 1) {
+  if constexpr (PIECES == 1) {
     // 16-byte fragments: A and B fragments of a substep double-buffered (fa/fb).
     Frag8 fa, fb;
     Scales8 sa0, sa1;
@@ -615,6 +540,197 @@ __global__ void __launch_bounds__(256)
 #endif
 }
 
+// ---- 256x256 kernel, A by LDS DMA (BF16, FP16, INT8 on 16x16 MFMAs) --------
+
+// The staged kernel's shape rules, on 16x16 MFMAs, with A moved from global
+// memory into LDS by LDS-DMA loads (buffer_load_dwordx4 ... lds) instead of
+// through registers and ds_write: half the stage writes disappear, and the
+// freed registers double-buffer the MFMA fragments.
+//
+// The 16x16 BF16/FP16/INT8 MFMAs are issued in their in-place form (Op::
+// mma_tied): the compiler does not tie these instructions' accumulator input
+// to their output, and at 256 accumulator registers the copies it makes
+// instead spill. Program order is then the issue order (every MFMA is its own
+// scheduling region), and the kernel keeps the hazard distances the compiler
+// cannot see: operands come straight from LDS reads (whose waits the compiler
+// inserts for any reader), and ordered fences (acc_hazard_fence) separate the
+// accumulators' zeroing from the first MFMA and the last MFMA from the
+// epilogue's reads.
+//
+// LDS: a ring of three A slots, then two B stages, each 256 rows x 128 bytes
+// (160 KiB in all), with the staged kernel's XOR swizzle. A DMA writes 1 KiB
+// per instruction, lane l at +16*l, i.e. 8 rows; lane l therefore loads the
+// logical chunk that belongs at its physical position in that row.
+//
+// Per K step kt (A slot kt % 3, B stage kt & 1):
+//   substep 0: B registers holding step kt+1 are written to B stage s^1, and
+//              reloaded with step kt+3; barrier after it (publishes step kt+1,
+//              and ends every read of A slot kt % 3 and of B stage s^1's
+//              previous step);
+//   substep 1: A of step kt+3 is DMAed into slot kt % 3 (freed by that
+//              barrier), then the rest of step kt+3's B loads.
+// A step's DMAs are issued before its last B loads, so the in-order waits for
+// those loads, which the B stage writes of step kt+2 take before the barrier
+// that publishes step kt+3, also cover the DMAs.
+template <class Op>
+__global__ void __launch_bounds__(256)
+    gemm_dma16_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
+                      const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
+                      int group_m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, KS = 2;
+  static_assert(Op::M == 16 && Op::LANE_BYTES == 16 && MfmaGeometry<Op>::K_BYTES == 64 && !Op::SCALED,
+                "unscaled 16x16 instructions with 16-byte fragments");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * REGION];
+  if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
+
+  int tile_m, tile_n;
+  band_tile(M / BM, N / BM, group_m, tile_m, tile_n);
+  const int m0 = tile_m * BM, n0 = tile_n * BM;
+  const int row_bytes = K * Op::ELEM_BITS / 8;
+  const int k_steps = row_bytes / ROWB, last = k_steps - 1;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BM * row_bytes);
+  // B: load j of a step covers rows 32j .. 32j+31; thread t moves row 32j + t/8, chunk t%8.
+  const int voff = (t >> 3) * row_bytes + (t & 7) * 16;
+  uint8_t* const wb = lds + 3 * REGION + (t >> 3) * ROWB + (((t & 7) ^ ((t >> 4) & 7)) << 4);
+  auto load = [&](i32x4 (&v)[NB], int kt, int j) __attribute__((always_inline)) {
+    v[j] = __builtin_bit_cast(i32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(rb, voff, kt * ROWB + j * 32 * row_bytes, 0));
+  };
+  auto store = [&](const i32x4 (&v)[NB], int s, int j) __attribute__((always_inline)) {
+    *reinterpret_cast<i32x4*>(wb + s * REGION + j * 32 * ROWB) = v[j];
+  };
+  // A: wave w DMAs rows 64w .. 64w+63 of a step, instruction i rows 64w+8i ..
+  // +7; lane l is row 64w + 8i + l/8 at physical chunk l%8, whose swizzle is
+  // ((8i + l/8) >> 1) & 7 = (l/8 >> 1) | 4(i & 1).
+  const int arow = lane >> 3;
+  const int avoff0 = arow * row_bytes + (((lane & 7) ^ (arow >> 1)) << 4);
+  const int avoff1 = arow * row_bytes + (((lane & 7) ^ ((arow >> 1) | 4)) << 4);
+  const uint32_t lds_base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
+  auto dma_a = [&](int slot, int kt, int i) __attribute__((always_inline)) {
+    const int row = 64 * wave + 8 * i;
+    dma16(ra, (i & 1) ? avoff1 : avoff0, kt * ROWB + row * row_bytes, lds_base + slot * REGION + row * ROWB);
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lrow16 = lane & 15, lgroup16 = lane >> 4;
+  const int sw16 = ((lrow16 >> 1) & 7) ^ lgroup16;
+  // Fragment f of substep ks: its row's logical chunk ks*4 + lane group, so the
+  // lane base XOR (ks*4 << 4); fragments are 16 rows (2 KiB) apart. The A slot
+  // base is added per step; B's stage and fragment offsets are immediates.
+  const uint32_t ra16 = (wm * 128 + lrow16) * ROWB + (sw16 << 4);
+  const uint32_t rb16 = 3 * REGION + (wn * 128 + lrow16) * ROWB + (sw16 << 4);
+  auto frag_a = [&](int slot, int ks, int f) __attribute__((always_inline)) {
+    return *reinterpret_cast<const i32x4*>(lds + (ra16 ^ (static_cast<uint32_t>(ks) << 6)) + slot * REGION +
+                                           f * 16 * ROWB);
+  };
+  auto frag_b = [&](int s, int ks, int f) __attribute__((always_inline)) {
+    return *reinterpret_cast<const i32x4*>(lds + (rb16 ^ (static_cast<uint32_t>(ks) << 6)) + s * REGION +
+                                           f * 16 * ROWB);
+  };
+
+  typename Op::Acc acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = typename Op::Acc{};
+
+  // Prologue: A of steps 0..2 into slots 0..2, B of steps 0 and 1 in flight,
+  // step 0 written to B stage 0 (its load waits also cover the older DMAs),
+  // step 2's B into v0.
+  i32x4 v0[NB], v1[NB];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma_a(p, min(p, last), i);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v1, min(1, last), j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) store(v0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v0, min(2, last), j);
+  lds_barrier();
+
+  // Fragments are double-buffered by substep (set p = ks: two substeps per
+  // step and two steps per loop trip keep the parity static). The next
+  // substep's sixteen reads are spread over rows 0..5 of the current one, so
+  // they have landed by the barrier (whose LDS wait then costs nothing) and by
+  // the next substep's first MFMAs.
+  i32x4 fa[2][8], fb[2][8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    fa[0][f] = frag_a(0, 0, f);
+    fb[0][f] = frag_b(0, 0, f);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
+
+  // Slots of rows 0..5 (48 MFMAs, each its own scheduling region) carry the
+  // memory work: the next substep's fragment reads in every third slot; in
+  // substep 0 the B stage writes (every sixth) and the first half of step
+  // kt+3's B loads, each behind the write that frees its registers; in
+  // substep 1 the A DMAs of step kt+3 and then the rest of its B loads. Rows
+  // 6 and 7 are MFMAs only.
+  int slot = 0;  // A slot of the current step: kt % 3
+  auto step = [&](int kt, int s, i32x4 (&vnext)[NB]) __attribute__((always_inline)) {
+    const int next_slot = slot == 2 ? 0 : slot + 1;
+    static_for<0, KS>([&](auto ks_c) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ks_c)::value, p = ks, np = ks ^ 1;
+      const int na = ks == 0 ? slot : next_slot, nb = ks == 0 ? s : s ^ 1;
+      constexpr int nks = ks == 0 ? 1 : 0;
+      static_for<0, 64>([&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int q = decltype(slot_c)::value, i = q / 8, j = q % 8;
+        if constexpr (q < 48 && q % 3 == 0) {
+          constexpr int f = q / 3;  // 0..15: A fragments, then B
+          if constexpr (f < 8)
+            fa[np][f] = frag_a(na, nks, f);
+          else
+            fb[np][f - 8] = frag_b(nb, nks, f - 8);
+        }
+        if constexpr (ks == 0 && q < 48 && q % 6 == 1) store(vnext, s ^ 1, q / 6);
+        if constexpr (ks == 0 && q < 48 && q % 12 == 2) load(vnext, min(kt + 3, last), q / 12);
+        if constexpr (ks == 1 && q < 24 && q % 3 == 1) dma_a(slot, min(kt + 3, last), q / 3);
+        if constexpr (ks == 1 && q >= 26 && q < 48 && (q - 26) % 6 == 0)
+          load(vnext, min(kt + 3, last), 4 + (q - 26) / 6);
+        Op::mma_tied(fa[p][i], fb[p][j], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if constexpr (ks == 0) lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    slot = next_slot;
+  };
+  for (int kt = 0; kt < k_steps; kt += 2) {
+    step(kt, 0, v1);
+    step(kt + 1, 1, v0);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < Op::ACC_REGS; ++r) {
+        const int row = m0 + wm * 128 + i * 16 + Op::out_row(lane, r);
+        const int col = n0 + wn * 128 + j * 16 + lrow16;
+        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+      }
+#endif
+}
+
 // Launchers size their own grid: one workgroup per output tile of their kernel.
 using GemmLauncher = void (*)(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, void*, int, int, int,
                               int, hipStream_t);
@@ -630,11 +746,25 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
+// The 256x256 fast-path kernel of an instruction: the A-by-DMA kernel for the
+// 16x16 forms, the register-staged kernel for the 32x32 ones.
+template <class Op>
+const void* fast_kernel() {
+  if constexpr (Op::M == 16)
+    return reinterpret_cast<const void*>(gemm_dma16_kernel<Op>);
+  else
+    return reinterpret_cast<const void*>(gemm_staged_kernel<Op>);
+}
+
 template <class Op>
 void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m,
                         int n, int k, int group_m, hipStream_t stream) {
-  gemm_staged_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
-      a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+  if constexpr (Op::M == 16)
+    gemm_dma16_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
+        a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+  else
+    gemm_staged_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
+        a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
 // What a variant's fast launcher needs beyond a shape that divides its tile.
@@ -676,7 +806,7 @@ struct GemmVariant {
   GemmVariant{FMT,                                                                                           \
               mb_gemm_config{256, 256, BK, 256},                                                             \
               NAME,                                                                                          \
-              reinterpret_cast<const void*>(gemm_staged_kernel<SOP>),                                        \
+              fast_kernel<SOP>(),                                                                            \
               launch_gemm_staged<SOP>,                                                                       \
               launch_gemm<OP, CM, CN, BK, 2, 2, true>,                                                       \
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
