@@ -125,6 +125,26 @@ def test_gemm_matches_oracle_every_tile_and_ragged_shapes(gpu, dtype):
             _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8"])
+def test_fast_path_over_step_counts(gpu, dtype):
+    """The 256x256 fast path (A through a three-slot LDS ring for BF16/FP16/INT8,
+    two register-staged stages for FP8) at K step counts 4, 6, 10, 12 and 14,
+    which wrap the three-slot ring at every phase, on lattice operands (exact),
+    with M != N so a transposed tile order would show."""
+    from triton_chip_benchmarks_amd import _native
+
+    rng = np.random.default_rng(23)
+    config = max(_configs(dtype), key=lambda c: c["tile_m"] * c["tile_n"])
+    elements_per_step = 128 * 8 // {"bf16": 16, "fp16": 16, "int8": 8, "fp8": 8}[dtype]
+    for steps in (4, 6, 10, 12, 14):
+        m, n, k = 512, 768, steps * elements_per_step
+        launched = _native.gemm_launched_kernel(dtype, config, m, n, k)
+        assert not launched.endswith("_checked"), launched
+        print(f"gemm {dtype} fast path {m}x{n}x{k} ({steps} K steps) via {launched}", flush=True)
+        got, a_values, b_values = _run_gemm(dtype, config, m, n, k, rng)
+        _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
 def test_gemm_normal_operands_every_tile_elementwise(gpu, dtype):
     """N(0,1) operands: every entry within rtol = atol = GEMM_TOLERANCE[dtype] of the float64 oracle."""
