@@ -784,6 +784,7 @@ struct GemmVariant {
   int path;
   const char* checked_name;
   const void* checked_kernel;
+  int default_group;  // band height in tile rows when the caller passes 0 (measured per kernel)
 };
 
 #define MB_GEMM(FMT, OP, BM, BN, BK, WM, WN, NAME)                                                           \
@@ -797,12 +798,13 @@ struct GemmVariant {
               OP::ELEM_BITS,                                                                                 \
               kLdsPath,                                                                                      \
               NAME "_checked",                                                                               \
-              reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, true>)}
+              reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, true>),                      \
+              8}
 
 // 256x256 tiles: the staged kernel (BK = 128 bytes of K; instruction SOP) for
 // exact shapes, a checked LDS-staged kernel (tile CM x CN, instruction OP) for
 // the rest.
-#define MB_GEMM_STAGED(FMT, SOP, OP, BK, CM, CN, NAME, CNAME)                                                     \
+#define MB_GEMM_STAGED(FMT, SOP, OP, BK, CM, CN, GROUP, NAME, CNAME)                                              \
   GemmVariant{FMT,                                                                                           \
               mb_gemm_config{256, 256, BK, 256},                                                             \
               NAME,                                                                                          \
@@ -812,26 +814,29 @@ struct GemmVariant {
               static_cast<int>(sizeof(typename OP::Out)),                                                    \
               OP::ELEM_BITS,                                                                                 \
               kStagedPath,                                                                                   \
-              CNAME,                                                                               \
-              reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>)}
+              CNAME,                                                                                         \
+              reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>),                        \
+              GROUP}
+// GROUP: the band height the 8192^3 sweep of 2..32 tile rows measured best per
+// fast-path kernel (INT8 4, FP8 6, the others 8; within about 2% of each other).
 const GemmVariant kGemmVariants[] = {
-    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16x16, MfmaBf16, 64, 256, 256, "gemm_bf16_256x256x64",
+    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16x16, MfmaBf16, 64, 256, 256, 8, "gemm_bf16_256x256x64",
                    "gemm_bf16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
-    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16x16, MfmaF16, 64, 256, 256, "gemm_f16_256x256x64",
+    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16x16, MfmaF16, 64, 256, 256, 8, "gemm_f16_256x256x64",
                    "gemm_f16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8, MfmaFp8, 128, 256, 256, "gemm_fp8_256x256x128",
+    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8, MfmaFp8, 128, 256, 256, 6, "gemm_fp8_256x256x128",
                    "gemm_fp8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
-    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8x16, MfmaI8, 128, 256, 256, "gemm_i8_256x256x128",
+    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8x16, MfmaI8, 128, 256, 256, 4, "gemm_i8_256x256x128",
                    "gemm_i8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
-    MB_GEMM_STAGED(MB_MATRIX_MXFP4, MfmaMxfp4, MfmaMxfp4, 256, 128, 128, "gemm_mxfp4_256x256x256",
+    MB_GEMM_STAGED(MB_MATRIX_MXFP4, MfmaMxfp4, MfmaMxfp4, 256, 128, 128, 8, "gemm_mxfp4_256x256x256",
                    "gemm_mxfp4_128x128x256_checked"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, "gemm_mxfp4_128x128x256"),
@@ -955,7 +960,7 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
     if (scale_a_bytes < blocks * m * 8 || scale_b_bytes < blocks * n * 8)
       return fail(MB_ERR_INVALID, "mb_gemm: scale buffers too small ([ceil(K/256)][M|N][8] bytes needed)");
   }
-  const int group = group_m ? static_cast<int>(group_m) : 8;
+  const int group = group_m ? static_cast<int>(group_m) : variant->default_group;
   choice.launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
                 static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
                 group, static_cast<hipStream_t>(stream));
