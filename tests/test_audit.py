@@ -114,8 +114,10 @@ def test_registered_names_follow_the_mangled_template_arguments():
         == "gemm_mxfp4_128x128x256_checked"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIDv4_jLi1ELi1EEEv") == "copy_dwordx4_vpt1_nt"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIjLi8ELi2EEEv") == "copy_dword_vpt8_stream"
-    assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_9MfmaMxfp4ELi128ELi2ELi4EEEv") \
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_118gemm_staged_kernelINS_9MfmaMxfp4EEEvPKh") \
         == "gemm_mxfp4_256x256x256"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_117gemm_dma16_kernelINS_11MfmaBf16x16EEEvPKh") \
+        == "gemm_bf16_256x256x64"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
     assert audit.registered_name("unrelated_symbol") is None
 

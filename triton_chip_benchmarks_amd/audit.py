@@ -29,7 +29,6 @@ _MFMA_FORMAT = {"MfmaBf16": "bf16", "MfmaF16": "f16", "MfmaI8": "i8", "MfmaFp8":
                 "MfmaMxfp4": "mxfp4", "MfmaF32": "f32", "MfmaF64": "f64"}
 _PEAK_RE = re.compile(r"tensor_peak_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
 _GEMM_RE = re.compile(r"gemm_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
-_GEMM_DMA_RE = re.compile(r"gemm_dma_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)E")
 _GEMM_STAGED_RE = re.compile(r"gemm_(?:staged|dma16)_kernelINS_\d+(Mfma\w+?)EE")
 _ELEM_BITS = {"bf16": 16, "f16": 16, "i8": 8, "fp8": 8, "mxfp4": 4, "f32": 32, "f64": 64}
 _COPY_RE = re.compile(r"copy_kernelI(Dv4_j|j|h)Li(\d+)ELi([012])E")
@@ -51,11 +50,6 @@ def registered_name(symbol: str) -> str | None:
     if match:
         op, bm, bn, bk, _wm, _wn, checked = match.groups()
         return f"gemm_{_MFMA_FORMAT[op]}_{bm}x{bn}x{bk}{'_checked' if checked == '1' else ''}"
-    match = _GEMM_DMA_RE.search(symbol)
-    if match:
-        op, row_bytes, _wm, _wn = match.groups()
-        fmt = _MFMA_FORMAT[op]
-        return f"gemm_{fmt}_256x256x{int(row_bytes) * 8 // _ELEM_BITS[fmt]}"
     match = _GEMM_STAGED_RE.search(symbol)
     if match:
         fmt = _MFMA_FORMAT[match.group(1).removesuffix("x16")]
