@@ -116,7 +116,7 @@ def test_registered_names_follow_the_mangled_template_arguments():
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_111copy_kernelIjLi8ELi2EEEv") == "copy_dword_vpt8_stream"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_118gemm_staged_kernelINS_9MfmaMxfp4EEEvPKh") \
         == "gemm_mxfp4_256x256x256"
-    assert audit.registered_name("_ZN2mb12_GLOBAL__N_117gemm_dma16_kernelINS_11MfmaBf16x16EEEvPKh") \
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_11MfmaBf16x16EEEvPKh") \
         == "gemm_bf16_256x256x64"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
     assert audit.registered_name("unrelated_symbol") is None
@@ -204,20 +204,22 @@ def test_no_packed_fp32_valu_anywhere():
     assert not re.search(r"\bv_pk_(?:add|mul|fma|mov)_f32\b", text)
 
 
-@pytest.mark.parametrize("name,instruction", [("gemm_bf16_256x256x64", "v_mfma_f32_16x16x32_bf16"),
-                                              ("gemm_f16_256x256x64", "v_mfma_f32_16x16x32_f16"),
-                                              ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8")])
-def test_staged_16x16_gemm_loop_has_no_accumulator_copies(listing, name, instruction):
-    """The in-place 16x16 MFMAs keep every accumulator in its AGPRs: the K loop
-    (two 128-byte steps) issues 256 MFMAs, 64 fragment reads, 16 B stage
-    writes and 32 buffer loads (16 of B into registers, 16 LDS-DMA of A) and
-    nothing else on the vector side, with no spills."""
+@pytest.mark.parametrize("name,instruction,mfmas", [("gemm_bf16_256x256x64", "v_mfma_f32_16x16x32_bf16", 256),
+                                                     ("gemm_f16_256x256x64", "v_mfma_f32_16x16x32_f16", 256),
+                                                     ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8", 256),
+                                                     ("gemm_fp8_256x256x128", "v_mfma_f32_32x32x64_f8f6f4", 64)])
+def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfmas):
+    """The A-by-DMA fast path keeps every accumulator in its AGPRs (the 16x16
+    forms through their in-place assembly): the K loop (two 128-byte steps)
+    issues its MFMAs, 64 fragment reads, 16 B stage writes and 32 buffer loads
+    (16 of B into registers, 16 LDS-DMA of A) and nothing else on the vector
+    side but the A slot address, with no spills."""
     assert name in listing
     resources = audit.resources(name)
     assert resources["register_spills"] == 0 and resources["scratch_bytes"] == 0
     summary = audit.loop_summary(name)
     assert summary["timed_loop_matrix_types"] == [instruction]
-    assert summary["timed_loop_matrix_instructions"] == 256
+    assert summary["timed_loop_matrix_instructions"] == mfmas
     vector = dict(summary["timed_loop_vector_memory_or_alu"])
     assert {k: vector.pop(k, 0) for k in ("ds_read_b128", "ds_write_b128", "buffer_load_dwordx4")} == \
         {"ds_read_b128": 64, "ds_write_b128": 16, "buffer_load_dwordx4": 32}

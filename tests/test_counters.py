@@ -15,7 +15,7 @@ from triton_chip_benchmarks_amd import counters
 
 COPY = ("void mb::(anonymous namespace)::copy_kernel<unsigned int __vector(4), 1, 2>"
         "(unsigned int __vector(4) const*, unsigned int __vector(4)*, unsigned long)")
-GEMM = ("void mb::(anonymous namespace)::gemm_dma16_kernel<mb::MfmaBf16x16>(unsigned char const*, "
+GEMM = ("void mb::(anonymous namespace)::gemm_dma_kernel<mb::MfmaBf16x16>(unsigned char const*, "
         "unsigned char const*, unsigned char const*, unsigned char const*, mb::MfmaBf16x16::Out*, int, int, int, int)")
 FIELDS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
           "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",

@@ -13,11 +13,11 @@
 // timing by the caller).
 //
 // Two kernels:
-//   * gemm_dma16_kernel (BF16, FP16, INT8) and gemm_staged_kernel (FP8,
-//     MXFP4): 256x256 tiles when the shape divides the tile. Four waves, one
-//     per SIMD, each owning 128x128 outputs in AGPRs: 64 accumulators of
-//     16x16 (the 16x16 instructions sustain a higher clock under the power
-//     limit) or 16 of 32x32. In the staged kernel operands flow
+//   * gemm_dma_kernel (BF16, FP16, INT8 on 16x16 MFMAs; FP8 on 32x32) and
+//     gemm_staged_kernel (MXFP4): 256x256 tiles when the shape divides the
+//     tile. Four waves, one per SIMD, each owning 128x128 outputs in AGPRs:
+//     64 accumulators of 16x16 (the 16x16 instructions sustain a higher clock
+//     under the power limit) or 16 of 32x32. In the staged kernel operands flow
 //     global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128 bytes of every
 //     row) is loaded two steps ahead into one of two register sets, written to
 //     one of two LDS stages a step ahead, and read back as fragments ahead of
@@ -265,7 +265,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// ---- VGPR-staged 256x256 kernel (FP8, MXFP4) -------------------------------
+// ---- VGPR-staged 256x256 kernel (MXFP4) ------------------------------------
 
 // C = A . B^T for M, N multiples of 256, K * bits a multiple of 1024 (128-byte
 // K steps) with an even number of at least 4 steps; A, B byte offsets and the
@@ -295,8 +295,7 @@ __global__ void __launch_bounds__(256)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NL = 16;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
   constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = Op::SCALED ? 4 : 0;
-  static_assert(Op::M == 32 && ((PIECES == 1 && KS == 4) || (PIECES == 2 && KS == 2 && !Op::SCALED)),
-                "16-byte fragments in four substeps, or unscaled 32-byte fragments in two");
+  static_assert(Op::M == 32 && PIECES == 1 && KS == 4, "32x32 instructions with 16-byte fragments in four substeps");
   constexpr int TILES = 4;  // 32x32 fragments per wave side
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * REGION + SCALE_RING * SCALE_STAGE];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written (scale) reads live; never executed
@@ -403,7 +402,7 @@ __global__ void __launch_bounds__(256)
   load(v0, 2, 0, NL);
   lds_barrier();
 
-  if constexpr (PIECES == 1) {
+  {
     // 16-byte fragments: A and B fragments of a substep double-buffered (fa/fb).
     Frag8 fa, fb;
     Scales8 sa0, sa1;
@@ -465,66 +464,6 @@ __global__ void __launch_bounds__(256)
       step(kt, 0, v1, sa0, sa1);
       step(kt + 1, 1, v0, sa1, sa0);
     }
-  } else {
-    // 32-byte fragments (two substeps per step): A fragments double-buffered,
-    // B fragments in one set, B_j refilled with the next substep's B_j right
-    // after the four MFMAs that read it (a column). Each column is fenced so
-    // the refill cannot be hoisted above the MFMAs still reading the old B_j,
-    // and the column's share of the next A reads, stage writes and loads is
-    // interleaved with its MFMAs.
-    using F = typename Op::Frag;
-    F fa0[4], fa1[4], fbq[4];
-    auto read_frag = [&](uint32_t off, int s, int ks, int f) __attribute__((always_inline)) {
-      const uint32_t x0 = static_cast<uint32_t>(ks * (KB / 16)) << 4, x1 = x0 + 16;
-      const i32x4 lo = *reinterpret_cast<const i32x4*>(lds + (off ^ x0) + s * REGION + f * 32 * ROWB);
-      const i32x4 hi = *reinterpret_cast<const i32x4*>(lds + (off ^ x1) + s * REGION + f * 32 * ROWB);
-      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      fa0[f] = read_frag(ra_off, 0, 0, f);
-      fbq[f] = read_frag(rb_off, 0, 0, f);
-    }
-    auto step = [&](int kt, int s, i32x4 (&vnext)[NL]) __attribute__((always_inline)) {
-      static_for<0, KS>([&](auto ks_c) __attribute__((always_inline)) {
-        constexpr int ks = decltype(ks_c)::value;
-        F (&cur)[4] = (ks & 1) ? fa1 : fa0;
-        F (&nxt)[4] = (ks & 1) ? fa0 : fa1;
-        const int ns = ks + 1 < KS ? s : s ^ 1, nks = ks + 1 < KS ? ks + 1 : 0;
-        constexpr int W0 = ks == 0 ? 0 : NL, W1 = NL;  // all stage writes before the barrier
-        constexpr int L0 = ks * NL / KS, L1 = (ks + 1) * NL / KS;
-        static_for<0, 4>([&](auto j_c) __attribute__((always_inline)) {
-          constexpr int j = decltype(j_c)::value;
-          constexpr int CW0 = W0 + (W1 - W0) * j / 4, CW1 = W0 + (W1 - W0) * (j + 1) / 4;
-          constexpr int CL0 = L0 + (L1 - L0) * j / 4, CL1 = L0 + (L1 - L0) * (j + 1) / 4;
-          if constexpr (j == 0) {
-#pragma unroll
-            for (int f = 0; f < 4; ++f) nxt[f] = read_frag(ra_off, ns, nks, f);
-          }
-          store(vnext, s ^ 1, CW0, CW1);
-          load(vnext, min(kt + 3, last), CL0, CL1);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i][j] = Op::mma(cur[i], fbq[j], acc[i][j], 0, 0);
-          constexpr int RA = j == 0 ? 8 : 0, WR = CW1 - CW0, LD = CL1 - CL0;
-          static_for<0, 4>([&](auto q_c) __attribute__((always_inline)) {
-            constexpr int q = decltype(q_c)::value;
-            constexpr int NW = (q + 1) * WR / 4 - q * WR / 4, NLD = (q + 1) * LD / 4 - q * LD / 4;
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
-            if constexpr (RA > 0) __builtin_amdgcn_sched_group_barrier(0x100, RA / 4, 0);  // DS read
-            if constexpr (NW > 0) __builtin_amdgcn_sched_group_barrier(0x200, NW, 0);      // DS write
-            if constexpr (NLD > 0) __builtin_amdgcn_sched_group_barrier(0x020, NLD, 0);    // VMEM read
-          });
-          __builtin_amdgcn_sched_barrier(0);
-          fbq[j] = read_frag(rb_off, ns, nks, j);
-        });
-        if constexpr (ks == KS - 2) lds_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    };
-    for (int kt = 0; kt < k_steps; kt += 2) {
-      step(kt, 0, v1);
-      step(kt + 1, 1, v0);
-    }
   }
 
 #pragma unroll
@@ -540,22 +479,24 @@ __global__ void __launch_bounds__(256)
 #endif
 }
 
-// ---- 256x256 kernel, A by LDS DMA (BF16, FP16, INT8 on 16x16 MFMAs) --------
+// ---- 256x256 kernel, A by LDS DMA (BF16, FP16, INT8 on 16x16; FP8 on 32x32) --
 
-// The staged kernel's shape rules, on 16x16 MFMAs, with A moved from global
-// memory into LDS by LDS-DMA loads (buffer_load_dwordx4 ... lds) instead of
-// through registers and ds_write: half the stage writes disappear, and the
-// freed registers double-buffer the MFMA fragments.
+// The staged kernel's shape rules with A moved from global memory into LDS by
+// LDS-DMA loads (buffer_load_dwordx4 ... lds) instead of through registers and
+// ds_write: half the stage writes disappear, and the freed registers
+// double-buffer the MFMA fragments. Instructions whose K slice per substep is
+// 64 bytes of a 128-byte step: the 16x16 BF16/FP16/INT8 forms (16-byte
+// fragments, 8x8 per wave) and the 32x32 FP8 form (32-byte fragments, 4x4).
 //
 // The 16x16 BF16/FP16/INT8 MFMAs are issued in their in-place form (Op::
 // mma_tied): the compiler does not tie these instructions' accumulator input
 // to their output, and at 256 accumulator registers the copies it makes
-// instead spill. Program order is then the issue order (every MFMA is its own
-// scheduling region), and the kernel keeps the hazard distances the compiler
-// cannot see: operands come straight from LDS reads (whose waits the compiler
+// instead spill. The kernel keeps the hazard distances the compiler cannot see
+// for them: operands come straight from LDS reads (whose waits the compiler
 // inserts for any reader), and ordered fences (acc_hazard_fence) separate the
 // accumulators' zeroing from the first MFMA and the last MFMA from the
-// epilogue's reads.
+// epilogue's reads. Every MFMA is its own scheduling region, so program order
+// is the issue order.
 //
 // LDS: a ring of three A slots, then two B stages, each 256 rows x 128 bytes
 // (160 KiB in all), with the staged kernel's XOR swizzle. A DMA writes 1 KiB
@@ -574,13 +515,16 @@ __global__ void __launch_bounds__(256)
 // that publishes step kt+3, also cover the DMAs.
 template <class Op>
 __global__ void __launch_bounds__(256)
-    gemm_dma16_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
-                      const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
-                      int group_m) {
+    gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
+                    const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
+                    int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, KS = 2;
-  static_assert(Op::M == 16 && Op::LANE_BYTES == 16 && MfmaGeometry<Op>::K_BYTES == 64 && !Op::SCALED,
-                "unscaled 16x16 instructions with 16-byte fragments");
+  constexpr int TILES = 128 / Op::M, PIECES = Op::LANE_BYTES / 16;
+  static_assert(MfmaGeometry<Op>::K_BYTES == 64 && !Op::SCALED &&
+                    ((Op::M == 16 && PIECES == 1) || (Op::M == 32 && PIECES == 2)),
+                "unscaled instructions with a 64-byte K slice: 16x16 with 16-byte or 32x32 with 32-byte fragments");
+  using Frag = typename Op::Frag;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * REGION];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
 
@@ -618,27 +562,41 @@ __global__ void __launch_bounds__(256)
   };
 
   const int wm = wave & 1, wn = wave >> 1;
-  const int lrow16 = lane & 15, lgroup16 = lane >> 4;
-  const int sw16 = ((lrow16 >> 1) & 7) ^ lgroup16;
-  // Fragment f of substep ks: its row's logical chunk ks*4 + lane group, so the
-  // lane base XOR (ks*4 << 4); fragments are 16 rows (2 KiB) apart. The A slot
-  // base is added per step; B's stage and fragment offsets are immediates.
-  const uint32_t ra16 = (wm * 128 + lrow16) * ROWB + (sw16 << 4);
-  const uint32_t rb16 = 3 * REGION + (wn * 128 + lrow16) * ROWB + (sw16 << 4);
-  auto frag_a = [&](int slot, int ks, int f) __attribute__((always_inline)) {
-    return *reinterpret_cast<const i32x4*>(lds + (ra16 ^ (static_cast<uint32_t>(ks) << 6)) + slot * REGION +
-                                           f * 16 * ROWB);
+  const int lrow = lane % Op::M, lgroup = lane / Op::M;
+  // Piece p of a lane's fragment in substep ks is its row's logical chunk
+  // ks*4 + lgroup*PIECES + p: the lane base XOR (ks << 6) XOR (p << 4), since
+  // the first chunk is even when PIECES = 2. Fragments are M rows apart; the
+  // A slot base is added per step, B's stage and fragment offsets are
+  // immediates.
+  const int sw = ((lrow >> 1) & 7) ^ (lgroup * PIECES);
+  const uint32_t ra0 = (wm * 128 + lrow) * ROWB + (sw << 4);
+  const uint32_t rb0 = 3 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
+  auto frag = [&](uint32_t base, int region, int ks, int f) __attribute__((always_inline)) {
+    const uint8_t* p = lds + (base ^ (static_cast<uint32_t>(ks) << 6)) + region + f * Op::M * ROWB;
+    if constexpr (PIECES == 1) {
+      return *reinterpret_cast<const i32x4*>(p);
+    } else {
+      const uint8_t* q = lds + (base ^ (static_cast<uint32_t>(ks) << 6) ^ 16u) + region + f * Op::M * ROWB;
+      return __builtin_shufflevector(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(q), 0, 1,
+                                     2, 3, 4, 5, 6, 7);
+    }
   };
-  auto frag_b = [&](int s, int ks, int f) __attribute__((always_inline)) {
-    return *reinterpret_cast<const i32x4*>(lds + (rb16 ^ (static_cast<uint32_t>(ks) << 6)) + s * REGION +
-                                           f * 16 * ROWB);
+  auto frag_a = [&](int slot, int ks, int f) __attribute__((always_inline)) {
+    return frag(ra0, slot * REGION, ks, f);
+  };
+  auto frag_b = [&](int s, int ks, int f) __attribute__((always_inline)) { return frag(rb0, s * REGION, ks, f); };
+  auto mma = [&](const Frag& a, const Frag& b, typename Op::Acc& c) __attribute__((always_inline)) {
+    if constexpr (Op::M == 16)
+      Op::mma_tied(a, b, c);
+    else
+      c = Op::mma(a, b, c, 0, 0);
   };
 
-  typename Op::Acc acc[8][8];
+  typename Op::Acc acc[TILES][TILES];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = typename Op::Acc{};
+    for (int j = 0; j < TILES; ++j) acc[i][j] = typename Op::Acc{};
 
   // Prologue: A of steps 0..2 into slots 0..2, B of steps 0 and 1 in flight,
   // step 0 written to B stage 0 (its load waits also cover the older DMAs),
@@ -660,26 +618,34 @@ __global__ void __launch_bounds__(256)
 
   // Fragments are double-buffered by substep (set p = ks: two substeps per
   // step and two steps per loop trip keep the parity static). The next
-  // substep's sixteen reads are spread over rows 0..5 of the current one, so
-  // they have landed by the barrier (whose LDS wait then costs nothing) and by
-  // the next substep's first MFMAs.
-  i32x4 fa[2][8], fb[2][8];
+  // substep's reads are spread over the first three quarters of the current
+  // one, so they have landed by the barrier (whose LDS wait then costs
+  // nothing) and by the next substep's first MFMAs.
+  Frag fa[2][TILES], fb[2][TILES];
 #pragma unroll
-  for (int f = 0; f < 8; ++f) {
+  for (int f = 0; f < TILES; ++f) {
     fa[0][f] = frag_a(0, 0, f);
     fb[0][f] = frag_b(0, 0, f);
   }
+  if constexpr (Op::M == 16) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
+      for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
+  }
 
-  // Slots of rows 0..5 (48 MFMAs, each its own scheduling region) carry the
-  // memory work: the next substep's fragment reads in every third slot; in
-  // substep 0 the B stage writes (every sixth) and the first half of step
-  // kt+3's B loads, each behind the write that frees its registers; in
-  // substep 1 the A DMAs of step kt+3 and then the rest of its B loads. Rows
-  // 6 and 7 are MFMAs only.
+  // MFMA slots (one MFMA each, its own scheduling region) carry the memory
+  // work in their first three quarters: the next substep's fragment reads; in
+  // substep 0 the B stage writes and the first half of step kt+3's B loads,
+  // each behind the write that frees its registers; in substep 1 the A DMAs
+  // of step kt+3 and then the rest of its B loads. The last quarter is MFMAs
+  // only.
+  //   16x16 (64 slots): a fragment read every third slot of the first 48;
+  //     writes every sixth (from 1), loads every twelfth (from 2); DMAs every
+  //     third of the first 24 (from 1), the second-half loads every sixth from 26.
+  //   32x32 (16 slots): fragment f (two reads) in slot f of the first 8;
+  //     write j in slot j, load j in slot 2j+1; DMA i in slot i, the
+  //     second-half loads in slots 8..11.
   int slot = 0;  // A slot of the current step: kt % 3
   auto step = [&](int kt, int s, i32x4 (&vnext)[NB]) __attribute__((always_inline)) {
     const int next_slot = slot == 2 ? 0 : slot + 1;
@@ -687,21 +653,27 @@ __global__ void __launch_bounds__(256)
       constexpr int ks = decltype(ks_c)::value, p = ks, np = ks ^ 1;
       const int na = ks == 0 ? slot : next_slot, nb = ks == 0 ? s : s ^ 1;
       constexpr int nks = ks == 0 ? 1 : 0;
-      static_for<0, 64>([&](auto slot_c) __attribute__((always_inline)) {
-        constexpr int q = decltype(slot_c)::value, i = q / 8, j = q % 8;
-        if constexpr (q < 48 && q % 3 == 0) {
-          constexpr int f = q / 3;  // 0..15: A fragments, then B
-          if constexpr (f < 8)
-            fa[np][f] = frag_a(na, nks, f);
+      static_for<0, TILES * TILES>([&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int q = decltype(slot_c)::value, i = q / TILES, j = q % TILES;
+        constexpr bool w16 = TILES == 8;
+        constexpr int fr = w16 ? (q < 48 && q % 3 == 0 ? q / 3 : -1) : (q < 8 ? q : -1);
+        if constexpr (fr >= 0) {
+          if constexpr (fr < TILES)
+            fa[np][fr] = frag_a(na, nks, fr);
           else
-            fb[np][f - 8] = frag_b(nb, nks, f - 8);
+            fb[np][fr - TILES] = frag_b(nb, nks, fr - TILES);
         }
-        if constexpr (ks == 0 && q < 48 && q % 6 == 1) store(vnext, s ^ 1, q / 6);
-        if constexpr (ks == 0 && q < 48 && q % 12 == 2) load(vnext, min(kt + 3, last), q / 12);
-        if constexpr (ks == 1 && q < 24 && q % 3 == 1) dma_a(slot, min(kt + 3, last), q / 3);
-        if constexpr (ks == 1 && q >= 26 && q < 48 && (q - 26) % 6 == 0)
-          load(vnext, min(kt + 3, last), 4 + (q - 26) / 6);
-        Op::mma_tied(fa[p][i], fb[p][j], acc[i][j]);
+        constexpr int wr = ks != 0 ? -1 : w16 ? (q < 48 && q % 6 == 1 ? q / 6 : -1) : (q < 8 ? q : -1);
+        if constexpr (wr >= 0) store(vnext, s ^ 1, wr);
+        constexpr int ld0 = ks != 0 ? -1 : w16 ? (q < 48 && q % 12 == 2 ? q / 12 : -1)
+                                               : (q < 8 && q % 2 == 1 ? q / 2 : -1);
+        if constexpr (ld0 >= 0) load(vnext, min(kt + 3, last), ld0);
+        constexpr int dm = ks != 1 ? -1 : w16 ? (q < 24 && q % 3 == 1 ? q / 3 : -1) : (q < 8 ? q : -1);
+        if constexpr (dm >= 0) dma_a(slot, min(kt + 3, last), dm);
+        constexpr int ld1 = ks != 1 ? -1 : w16 ? (q >= 26 && q < 48 && (q - 26) % 6 == 0 ? 4 + (q - 26) / 6 : -1)
+                                               : (q >= 8 && q < 12 ? 4 + q - 8 : -1);
+        if constexpr (ld1 >= 0) load(vnext, min(kt + 3, last), ld1);
+        mma(fa[p][i], fb[p][j], acc[i][j]);
         __builtin_amdgcn_sched_barrier(0);
       });
       if constexpr (ks == 0) lds_barrier();
@@ -713,19 +685,21 @@ __global__ void __launch_bounds__(256)
     step(kt, 0, v1);
     step(kt + 1, 1, v0);
   }
+  if constexpr (Op::M == 16) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc_hazard_fence(acc[i][j]);
+      for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
+  }
 
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < TILES; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < TILES; ++j)
 #pragma unroll
       for (int r = 0; r < Op::ACC_REGS; ++r) {
-        const int row = m0 + wm * 128 + i * 16 + Op::out_row(lane, r);
-        const int col = n0 + wn * 128 + j * 16 + lrow16;
+        const int row = m0 + wm * 128 + i * Op::M + Op::out_row(lane, r);
+        const int col = n0 + wn * 128 + j * Op::N + lrow;
         C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
       }
 #endif
@@ -747,11 +721,11 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
 }
 
 // The 256x256 fast-path kernel of an instruction: the A-by-DMA kernel for the
-// 16x16 forms, the register-staged kernel for the 32x32 ones.
+// unscaled ones, the register-staged kernel (with its scale ring) for MXFP4.
 template <class Op>
 const void* fast_kernel() {
-  if constexpr (Op::M == 16)
-    return reinterpret_cast<const void*>(gemm_dma16_kernel<Op>);
+  if constexpr (!Op::SCALED)
+    return reinterpret_cast<const void*>(gemm_dma_kernel<Op>);
   else
     return reinterpret_cast<const void*>(gemm_staged_kernel<Op>);
 }
@@ -759,8 +733,8 @@ const void* fast_kernel() {
 template <class Op>
 void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m,
                         int n, int k, int group_m, hipStream_t stream) {
-  if constexpr (Op::M == 16)
-    gemm_dma16_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
+  if constexpr (!Op::SCALED)
+    gemm_dma_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
         a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
   else
     gemm_staged_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
