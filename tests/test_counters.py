@@ -134,3 +134,38 @@ def test_by_grid_keeps_workgroup_counts_apart(tmp_path):
     assert apart["tensor_peak_bf16_128x128x64_c2_mfma16_kn@256wg"]["clock_ghz"] == pytest.approx(2.0)
     assert apart["tensor_peak_bf16_128x128x64_c2_mfma16_kn@1024wg"]["clock_ghz"] == pytest.approx(2.2)
     assert apart["tensor_peak_bf16_128x128x64_c2_mfma16_kn@1024wg"]["mfma_busy"] == pytest.approx(0.9)
+
+
+def test_optional_stall_and_path_passes(tmp_path):
+    """The issue-wait and memory-path passes add per-wave-cycle and per-CU-cycle fractions."""
+    cycles_per_xcd, duration = 1_000_000, 500_000
+    grbm = cycles_per_xcd * counters.XCDS
+    cu_cycles = cycles_per_xcd * counters.CUS
+    _write_pass(tmp_path / "stall", [
+        (1, GEMM, "GRBM_GUI_ACTIVE", grbm, duration), (1, GEMM, "SQ_WAVE_CYCLES", 1000, duration),
+        (1, GEMM, "SQ_WAIT_INST_ANY", 500, duration), (1, GEMM, "SQ_WAIT_INST_LDS", 70, duration),
+        (1, GEMM, "SQ_ACTIVE_INST_LDS", 120, duration), (1, GEMM, "SQ_ACTIVE_INST_VMEM", 50, duration),
+        (1, GEMM, "SQ_INSTS_MFMA", 64, duration), (1, GEMM, "SQ_ACTIVE_INST_VALU", 200, duration),
+        (1, GEMM, "SQ_INST_CYCLES_VMEM_RD", 40, duration)])
+    _write_pass(tmp_path / "path", [
+        (1, GEMM, "GRBM_GUI_ACTIVE", grbm, duration),
+        (1, GEMM, "TA_ADDR_STALLED_BY_TC_CYCLES_sum", 0.05 * cu_cycles, duration),
+        (1, GEMM, "TA_TA_BUSY_sum", 0.4 * cu_cycles, duration),
+        (1, GEMM, "TCP_TCC_READ_REQ_LATENCY_sum", 3_700_000, duration),
+        (1, GEMM, "TCP_TCC_READ_REQ_sum", 10_000, duration),
+        (1, GEMM, "TCP_PENDING_STALL_CYCLES_sum", 0.3 * cu_cycles, duration),
+        (1, GEMM, "TCC_TAG_STALL_sum", 1234, duration), (1, GEMM, "TD_TC_STALL_sum", 0.2 * cu_cycles, duration)])
+    summary = counters.summarize(tmp_path)
+    gemm = summary["kernels"]["gemm_bf16_256x256x64"]
+    assert gemm["wait_inst_frac"] == pytest.approx(0.5)
+    assert gemm["wait_inst_lds_frac"] == pytest.approx(0.07)
+    assert gemm["active_lds_frac"] == pytest.approx(0.12)
+    assert gemm["mfma_instructions"] == 64
+    assert gemm["l2_read_latency_cycles"] == pytest.approx(370)
+    assert gemm["ta_stalled_by_l1_frac"] == pytest.approx(0.05)
+    assert gemm["ta_busy_frac"] == pytest.approx(0.4)
+    assert gemm["l1_pending_stall_frac"] == pytest.approx(0.3)
+    assert gemm["l2_tag_stall_cycles"] == 1234
+    assert gemm["td_stalled_by_l1_frac"] == pytest.approx(0.2)
+    # Neither pass runs by default.
+    assert "stall" not in counters.DEFAULT_PASSES and "path" not in counters.DEFAULT_PASSES

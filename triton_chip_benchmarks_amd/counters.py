@@ -45,7 +45,8 @@ if __package__ in (None, ""):
 
 ROOT = Path(__file__).resolve().parent.parent
 XCDS = 8
-SIMDS = 256 * 4
+CUS = 256
+SIMDS = CUS * 4
 CALIBRATION_BYTES = 2**30  # the 1 GiB copy reads and writes this many bytes
 CALIBRATION_KERNELS = ("copy_dwordx4_vpt1_stream", "copy_dwordx4_vpt1_nt", "copy_dwordx4_vpt1")
 
@@ -57,7 +58,14 @@ PASSES = {
     "l2": ["GRBM_GUI_ACTIVE", "TCP_TCC_READ_REQ_sum", "TCC_HIT_sum", "TCC_MISS_sum", "TCC_REQ_sum"],
     "fetch": ["FETCH_SIZE"],
     "write": ["WRITE_SIZE"],
+    # Optional issue/wait breakdown (not in the default set): where a wave's cycles go besides MFMA issue.
+    "stall": ["GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_LDS",
+              "SQ_ACTIVE_INST_VMEM", "SQ_INSTS_MFMA", "SQ_ACTIVE_INST_VALU", "SQ_INST_CYCLES_VMEM_RD"],
+    # Optional memory-path pass: vector L1 -> L2 read latency and the stalls along the load path.
+    "path": ["GRBM_GUI_ACTIVE", "TA_ADDR_STALLED_BY_TC_CYCLES_sum", "TA_TA_BUSY_sum", "TCP_TCC_READ_REQ_LATENCY_sum",
+             "TCP_TCC_READ_REQ_sum", "TCP_PENDING_STALL_CYCLES_sum", "TCC_TAG_STALL_sum", "TD_TC_STALL_sum"],
 }
+DEFAULT_PASSES = ("sq", "l2", "fetch", "write")
 
 _MFMA_FORMAT = {"MfmaBf16": "bf16", "MfmaF16": "f16", "MfmaI8": "i8", "MfmaFp8": "fp8", "MfmaMxfp4": "mxfp4",
                 "MfmaF32": "f32", "MfmaF64": "f64"}
@@ -139,7 +147,7 @@ def rocprof_command(counters, out_dir: Path, program) -> list[str]:
 def collect(out: Path, program, passes=None, timeout_s: float = 300.0) -> None:
     out.mkdir(parents=True, exist_ok=True)
     env = dict(os.environ, TMPDIR="/tmp")
-    for name in passes or PASSES:
+    for name in passes or DEFAULT_PASSES:
         directory = out / name
         command = rocprof_command(PASSES[name], directory, program)
         print(f"[counters] pass {name}: {' '.join(PASSES[name])}", flush=True)
@@ -220,6 +228,8 @@ def summarize(out: Path, by_grid: bool = False) -> dict:
     summary = {}
     for kernel in kernels:
         sq, l2 = passes.get("sq", {}).get(kernel, {}), passes.get("l2", {}).get(kernel, {})
+        stall = passes.get("stall", {}).get(kernel, {})
+        path = passes.get("path", {}).get(kernel, {})
         row = {
             "dispatches": {name: len(data.get(kernel, {})) for name, data in passes.items()},
             "duration_ms": _mean([_per_dispatch(data.get(kernel, {}), lambda v: v["duration_ns"] / 1e6)
@@ -236,6 +246,29 @@ def summarize(out: Path, by_grid: bool = False) -> dict:
             "fetch_size_kib": _per_dispatch(fetch.get(kernel, {}), lambda v: v["FETCH_SIZE"]),
             "write_size_kib": _per_dispatch(write.get(kernel, {}), lambda v: v["WRITE_SIZE"]),
         }
+        if stall:
+            row.update({
+                "mfma_instructions": _per_dispatch(stall, lambda v: v["SQ_INSTS_MFMA"]),
+                "wait_inst_frac": _per_dispatch(stall, lambda v: v["SQ_WAIT_INST_ANY"] / v["SQ_WAVE_CYCLES"]),
+                "wait_inst_lds_frac": _per_dispatch(stall, lambda v: v["SQ_WAIT_INST_LDS"] / v["SQ_WAVE_CYCLES"]),
+                "active_lds_frac": _per_dispatch(stall, lambda v: v["SQ_ACTIVE_INST_LDS"] / v["SQ_WAVE_CYCLES"]),
+                "active_vmem_frac": _per_dispatch(stall, lambda v: v["SQ_ACTIVE_INST_VMEM"] / v["SQ_WAVE_CYCLES"]),
+                "active_valu_frac": _per_dispatch(stall, lambda v: v["SQ_ACTIVE_INST_VALU"] / v["SQ_WAVE_CYCLES"]),
+                "vmem_read_cycles_frac": _per_dispatch(
+                    stall, lambda v: v["SQ_INST_CYCLES_VMEM_RD"] / v["SQ_WAVE_CYCLES"]),
+            })
+        if path:
+            row.update({
+                "l2_read_latency_cycles": _per_dispatch(
+                    path, lambda v: v["TCP_TCC_READ_REQ_LATENCY_sum"] / v["TCP_TCC_READ_REQ_sum"]),
+                "ta_stalled_by_l1_frac": _per_dispatch(
+                    path, lambda v: v["TA_ADDR_STALLED_BY_TC_CYCLES_sum"] / (cycles(v) * CUS)),
+                "ta_busy_frac": _per_dispatch(path, lambda v: v["TA_TA_BUSY_sum"] / (cycles(v) * CUS)),
+                "l1_pending_stall_frac": _per_dispatch(
+                    path, lambda v: v["TCP_PENDING_STALL_CYCLES_sum"] / (cycles(v) * CUS)),
+                "l2_tag_stall_cycles": _per_dispatch(path, lambda v: v["TCC_TAG_STALL_sum"]),
+                "td_stalled_by_l1_frac": _per_dispatch(path, lambda v: v["TD_TC_STALL_sum"] / (cycles(v) * CUS)),
+            })
         if f_read and row["fetch_size_kib"] is not None:
             row["hbm_read_bytes"] = row["fetch_size_kib"] * 1024 / f_read
         if f_write and row["write_size_kib"] is not None:
