@@ -267,14 +267,14 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // ---- VGPR-staged 256x256 kernel (MXFP4) ------------------------------------
 
-// C = A . B^T for M, N multiples of 256, K * bits a multiple of 1024 (128-byte
-// K steps) with an even number of at least 4 steps; A, B byte offsets and the
-// MXFP4 scale blocks must fit in 31 bits. Four waves in a 2x2 grid own 128x128
-// outputs each.
+// C = A . B^T for MXFP4 operands with M, N multiples of 256, K a multiple of
+// 256 (128-byte K steps) with an even number of at least 4 steps; A, B byte
+// offsets and the scale blocks must fit in 31 bits. Four waves in a 2x2 grid
+// own 128x128 outputs each.
 //
 // LDS: regions [A stage 0][A stage 1][B stage 0][B stage 1] of 256 rows x 128
-// bytes (every stage and fragment offset is a ds_* immediate), then for MXFP4
-// a ring of four 4 KiB scale stages [256 A rows][256 B rows] x 8 bytes. Row r
+// bytes (every stage and fragment offset is a ds_* immediate), then a ring of
+// four 4 KiB scale stages [256 A rows][256 B rows] x 8 bytes. Row r
 // of a region holds its 16-byte chunk c at r*128 + ((c ^ ((r >> 1) & 7)) << 4),
 // so the 16 rows a ds_read_b128 quarter-wave touches hit 16 bank groups.
 //
@@ -294,8 +294,9 @@ __global__ void __launch_bounds__(256)
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NL = 16;
   constexpr int KB = MfmaGeometry<Op>::K_BYTES, KS = ROWB / KB, PIECES = Op::LANE_BYTES / 16;
-  constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = Op::SCALED ? 4 : 0;
-  static_assert(Op::M == 32 && PIECES == 1 && KS == 4, "32x32 instructions with 16-byte fragments in four substeps");
+  constexpr int SCALE_STAGE = 512 * 8, SCALE_RING = 4;
+  static_assert(Op::SCALED && Op::M == 32 && PIECES == 1 && KS == 4,
+                "scaled 32x32 instructions with 16-byte fragments in four substeps");
   constexpr int TILES = 4;  // 32x32 fragments per wave side
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * REGION + SCALE_RING * SCALE_STAGE];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written (scale) reads live; never executed
@@ -327,24 +328,18 @@ __global__ void __launch_bounds__(256)
       *reinterpret_cast<i32x4*>((j < 8 ? wa : wb) + s * REGION + (j & 7) * 32 * ROWB) = v[j];
   };
 
-  // MXFP4 scales: wave w DMAs 1 KiB of a step's scale stage, rows 128(w&1) ..
-  // +127 of A (w < 2) or B, from block kt of SA or SB.
-  __amdgpu_buffer_rsrc_t rs = ra;
-  int s_rows = 0, s_row0 = 0;
-  uint32_t scale_lds = 0;
-  if constexpr (Op::SCALED) {
-    const int blocks = k_steps;  // 256 E2M1 elements per 128-byte step
-    rs = wave < 2 ? buffer_rsrc(SA, blocks * M * 8) : buffer_rsrc(SB, blocks * N * 8);
-    s_rows = wave < 2 ? M : N;
-    s_row0 = (wave < 2 ? m0 : n0) + (wave & 1) * 128;
-    scale_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-                    (__attribute__((address_space(3))) uint8_t*)(lds + 4 * REGION))) + wave * 1024;
-  }
+  // Scales: wave w DMAs 1 KiB of a step's scale stage, rows 128(w&1) .. +127
+  // of A (w < 2) or B, from block kt of SA or SB (256 E2M1 elements, one
+  // 128-byte step, per block).
+  const __amdgpu_buffer_rsrc_t rs = wave < 2 ? buffer_rsrc(SA, k_steps * M * 8) : buffer_rsrc(SB, k_steps * N * 8);
+  const int s_rows = wave < 2 ? M : N;
+  const int s_row0 = (wave < 2 ? m0 : n0) + (wave & 1) * 128;
+  const uint32_t scale_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                                 (__attribute__((address_space(3))) uint8_t*)(lds + 4 * REGION))) + wave * 1024;
   // Block `block` into ring slot (slot & 3); past the last step the block is
   // clamped but the slot is not, so a slot still being read is never written.
   auto scale_dma = [&](int slot, int block) __attribute__((always_inline)) {
-    if constexpr (Op::SCALED)
-      dma16(rs, lane * 16, (block * s_rows + s_row0) * 8, scale_lds + (slot & 3) * SCALE_STAGE);
+    dma16(rs, lane * 16, (block * s_rows + s_row0) * 8, scale_lds + (slot & 3) * SCALE_STAGE);
   };
 
   const int wm = wave & 1, wn = wave >> 1;
@@ -367,20 +362,18 @@ __global__ void __launch_bounds__(256)
       fr[4 + f] = *reinterpret_cast<const i32x4*>(pb + f * 32 * ROWB);
     }
   };
-  // MXFP4: one dword per fragment row holding the scales of its lane's four
+  // One dword per fragment row holding the scales of its lane's four
   // 32-element groups of a step (groups lgroup, 2+lgroup, 4+lgroup, 6+lgroup:
   // substep ks uses byte ks), picked out of the row's 8 bytes by v_perm_b32.
   const uint32_t pick = 0x06040200u + 0x01010101u * static_cast<uint32_t>(lgroup);
   using Scales8 = uint32_t[8];
   auto read_scales = [&](Scales8& sc, int kt) __attribute__((always_inline)) {
-    if constexpr (Op::SCALED) {
-      const uint8_t* st = lds + 4 * REGION + (kt & 3) * SCALE_STAGE;
+    const uint8_t* st = lds + 4 * REGION + (kt & 3) * SCALE_STAGE;
 #pragma unroll
-      for (int f = 0; f < 8; ++f) {
-        const int row = f < 4 ? wm * 128 + f * 32 + lrow : 256 + wn * 128 + (f - 4) * 32 + lrow;
-        const i32x2 r = *reinterpret_cast<const i32x2*>(st + row * 8);
-        sc[f] = __builtin_amdgcn_perm(static_cast<uint32_t>(r[1]), static_cast<uint32_t>(r[0]), pick);
-      }
+    for (int f = 0; f < 8; ++f) {
+      const int row = f < 4 ? wm * 128 + f * 32 + lrow : 256 + wn * 128 + (f - 4) * 32 + lrow;
+      const i32x2 r = *reinterpret_cast<const i32x2*>(st + row * 8);
+      sc[f] = __builtin_amdgcn_perm(static_cast<uint32_t>(r[1]), static_cast<uint32_t>(r[0]), pick);
     }
   };
 
@@ -430,16 +423,12 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if constexpr (Op::SCALED)
-              acc[i][j] = Op::template mma_byte<ks>(cur[i], cur[4 + j], acc[i][j], sc[i], sc[4 + j]);
-            else
-              acc[i][j] = Op::mma(cur[i], cur[4 + j], acc[i][j], 0, 0);
-          }
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = Op::template mma_byte<ks>(cur[i], cur[4 + j], acc[i][j], sc[i], sc[4 + j]);
         // Interleave: after each MFMA, one of the next substep's fragment reads
         // (front-loaded; in the last substep also the next step's scale rows)
         // and this substep's writes and loads, evenly spaced.
-        constexpr int WR = W1 - W0, LD = L1 - L0, RD = (Op::SCALED && ks == KS - 1) ? 16 : 8;
+        constexpr int WR = W1 - W0, LD = L1 - L0, RD = ks == KS - 1 ? 16 : 8;
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                    // MFMA
