@@ -127,10 +127,10 @@ def test_gemm_matches_oracle_every_tile_and_ragged_shapes(gpu, dtype):
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8"])
 def test_fast_path_over_step_counts(gpu, dtype):
-    """The 256x256 fast path (A through a three-slot LDS ring for BF16/FP16/INT8,
-    two register-staged stages for FP8) at K step counts 4, 6, 10, 12 and 14,
-    which wrap the three-slot ring at every phase, on lattice operands (exact),
-    with M != N so a transposed tile order would show."""
+    """The 256x256 fast path (A through a three-slot LDS ring, B through
+    registers) at K step counts 4, 6, 10, 12 and 14, which wrap the three-slot
+    ring at every phase, on lattice operands (exact), with M != N so a
+    transposed tile order would show."""
     from triton_chip_benchmarks_amd import _native
 
     rng = np.random.default_rng(23)
@@ -143,6 +143,29 @@ def test_fast_path_over_step_counts(gpu, dtype):
         print(f"gemm {dtype} fast path {m}x{n}x{k} ({steps} K steps) via {launched}", flush=True)
         got, a_values, b_values = _run_gemm(dtype, config, m, n, k, rng)
         _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_band_height_orders_tiles_only(gpu, dtype):
+    """group_m orders the tiles and nothing else: every band height, including
+    ones taller than the tile rows and values near 2^32 (clamped by mb_gemm),
+    gives the same C on the fast path and on the checked path (ragged shape)."""
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+
+    rng = np.random.default_rng(31)
+    config = max(_configs(dtype), key=lambda c: c["tile_m"] * c["tile_n"])
+    for m, n, k in ((768, 512, 1024), (320, 448, 2 * config["tile_k"])):
+        launched = _native.gemm_launched_kernel(dtype, config, m, n, k)
+        print(f"gemm {dtype} band heights {m}x{n}x{k} via {launched}", flush=True)
+        got, a_values, b_values, (c, a, b) = _run_gemm(dtype, config, m, n, k, rng, keep_device=True)
+        _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
+        for group in (1, 2, 3, 7, 64, 2**31 + 5, 2**32 - 1):
+            c.fill_(-3)
+            _native.gemm(dtype, config, a, b, c, m, n, k, group_m=group)
+            torch.cuda.synchronize()
+            assert np.array_equal(c.cpu().numpy().astype(np.float64), got), group
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])

@@ -923,7 +923,12 @@ int mb_gemm(int format, const mb_gemm_config* config, const void* a, uint64_t a_
     if (scale_a_bytes < blocks * m * 8 || scale_b_bytes < blocks * n * 8)
       return fail(MB_ERR_INVALID, "mb_gemm: scale buffers too small ([ceil(K/256)][M|N][8] bytes needed)");
   }
-  const int group = group_m ? static_cast<int>(group_m) : variant->default_group;
+  // A band taller than the tile rows acts as the full height, so group_m is
+  // clamped to the row count of the smallest tile a launcher uses: the band's
+  // tile count (group x tile columns) then stays within the int grid.
+  const uint32_t max_group = (m + 63) / 64;
+  const int group = static_cast<int>(group_m ? (group_m < max_group ? group_m : max_group)
+                                             : static_cast<uint32_t>(variant->default_group));
   choice.launch(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<const uint8_t*>(scale_a),
                 static_cast<const uint8_t*>(scale_b), c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
                 group, static_cast<hipStream_t>(stream));
