@@ -21,6 +21,11 @@ in HBM. Each row is one configuration of the benchmark specification:
   peak_fp8_dense  the same kernel on the dense {+-0.5, +-1, +-2} set
   peak_mxfp4      17-row table: MXFP4 resident tile 128x128x256, 2 chains,
                               the reference's +-0.5/+-1 codes
+  vector_fp32, vector_fp16, vector_bf16, vector_fp64, vector_int8
+                  configs[1]  2^22 lanes (16 workgroups of 1024 per CU), 8
+                              independent accumulators x 4096 iterations of
+                              x = x*a + b, a0 ~ U[0.5, 1), a = 0.999, b = 1e-3
+                              (INT8: DP4A, x0 in [-4, 4], weights and bias 1)
 
 The resident tiles issue the 16x16 form of each MFMA (v_mfma_f32_16x16x32_bf16,
 v_mfma_f32_16x16x128_f8f6f4, v_mfma_scale_f32_16x16x128_f8f6f4): at the same
@@ -34,7 +39,9 @@ own fraction. Every output is validated before timing and again on the timed
 launches' output (bit-exact copy; exact FP8/INT8/MXFP4 GEMMs; elementwise
 |C-R| <= atol + rtol*|R| for BF16/FP16 (1e-2) and FP64 (1e-12) against a
 float64 device product; the resident tiles against their exact lattice
-reference under the reference's tolerance).
+reference under the reference's tolerance; FP32/FP64 vector chains against
+the closed form of the affine recurrence, FP16/BF16 sampled lanes bit-exact
+against a step-by-step recompute, INT8 exact).
 
 Timing, per kernel in turn (the reference's policy, common.py:459-461, warms
 for a device-time budget): untimed launches until at least --warmup launches
@@ -47,7 +54,8 @@ over --steps; min and median are over the sub-batch averages.
 cpu_baseline times the reference's own host arithmetic for each row on this
 machine's cores (torch.Tensor.copy_ of 1 GiB; torch.matmul in fp32, fp64
 for FP64, on sampled rows of the same GEMM shape or a batch of the same
-tiles), best repeat within a per-row budget.
+tiles; the recurrence vectorised by torch for the vector rows), best repeat
+within a per-row budget.
 """
 
 from __future__ import annotations
@@ -73,6 +81,8 @@ COPY_SEED = 0
 COPY_CONFIG = {"block_threads": 64, "vectors_per_thread": 1, "grid_blocks": 0, "nontemporal": "stream"}
 PEAK_ITERATIONS = 1024
 GEMM_SEED = 0
+VECTOR_ITERATIONS = 4096
+VECTOR_SEED = 0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_per_launch.txt"
 CPU_ROW_BUDGET_S = 2.0
 
@@ -265,6 +275,53 @@ class GemmWorkload(Workload):
         return cpu_baseline.gemm_sample_baseline(self.dtype, rows, self.size, self.size, CPU_ROW_BUDGET_S)
 
 
+class VectorWorkload(Workload):
+    """Independent FMA (INT8: DP4A) chains on the VALU: 16 workgroups of 1024 lanes per CU, 8 accumulators each."""
+
+    bound = "valu"
+    # Updates per loop trip: the suite sweep's best for each format.
+    UNROLL = {"fp32": 8, "fp16": 16, "bf16": 8, "fp64": 16, "int8": 16}
+    LABELS = {"fp32": "f32", "fp16": "f16", "bf16": "bf16", "fp64": "f64", "int8": "int8"}
+
+    def __init__(self, torch, compute_units, name, dtype):
+        from triton_chip_benchmarks_amd import _native, bench_vector
+
+        self.torch, self.bv, self.dtype, self.name = torch, bench_vector, dtype, name
+        self.row, self.label = f"vector_{dtype}", self.LABELS[dtype]
+        self.unit = "TOP/s" if dtype == "int8" else "TFLOP/s"
+        self.variant = bench_vector.VARIANTS[dtype][0]
+        self.kind, self.unroll, self.block = self.variant[0], self.UNROLL[dtype], 1024
+        self.elements = 16 * compute_units * self.block  # 2^22 lanes on 256 CUs
+        self.inputs, self.coefficients = bench_vector.make_inputs(dtype, self.elements, "cuda", "baseline",
+                                                                  VECTOR_SEED)
+        self.output = torch.empty_like(self.inputs)
+        self.kernel = _native.load().mb_vector_kernel_name(bench_vector.KINDS[self.kind], self.unroll).decode()
+        per_update = 8 if dtype == "int8" else 2  # bench_vector.py:1271-1273
+        self.work = per_update * bench_vector.CHAINS * self.elements * VECTOR_ITERATIONS
+        self.config = {"lanes": self.elements, "workgroups_per_cu": 16, "block": self.block,
+                       "accumulators": bench_vector.CHAINS, "iterations": VECTOR_ITERATIONS, "unroll": self.unroll,
+                       "operation": self.variant[1], "inputs": "x0 in [-4, 4], weights and bias 1" if dtype == "int8"
+                       else "x0 ~ U[0.5, 1), a = 0.999, b = 1e-3", "seed": VECTOR_SEED}
+
+    def launch(self):
+        self.bv.launch_vector(self.kind, self.inputs, self.output, self.coefficients, VECTOR_ITERATIONS, self.unroll,
+                              self.block)
+
+    def poison(self):
+        self.output.fill_(-(2**31) if self.dtype == "int8" else float("nan"))
+
+    def check(self):
+        self.torch.cuda.synchronize()
+        result = self.bv.validate(self.dtype, self.kind, self.inputs, self.output, self.coefficients,
+                                  VECTOR_ITERATIONS, "baseline", None)
+        return "; ".join(str(result[key]) for key in ("correctness", "step_recompute") if key in result)
+
+    def cpu(self):
+        from triton_chip_benchmarks_amd import cpu_baseline
+
+        return cpu_baseline.vector_baseline(self.dtype, 2**22, 8, CPU_ROW_BUDGET_S)
+
+
 def _row_specs():
     """(name, factory) in run order; factories take (torch, compute_units)."""
     def peak(name, dtype, tile, chains, per_cu, operands="lattice", mfma_m=16):
@@ -272,6 +329,9 @@ def _row_specs():
 
     def gemm(name, dtype, size):
         return name, lambda t, cu: GemmWorkload(t, cu, name, dtype, size)
+
+    def vector(name, dtype):
+        return name, lambda t, cu: VectorWorkload(t, cu, name, dtype)
 
     return [
         ("hbm_copy", CopyWorkload),
@@ -285,6 +345,7 @@ def _row_specs():
         peak("peak_fp8", "fp8", (128, 128, 128), 2, 4),
         peak("peak_fp8_dense", "fp8", (128, 128, 128), 2, 4, "dense"),
         peak("peak_mxfp4", "fp4", (128, 128, 256), 2, 4),
+        *(vector(f"vector_{dtype}", dtype) for dtype in ("fp32", "fp16", "bf16", "fp64", "int8")),
     ]
 
 
@@ -407,6 +468,10 @@ def main(argv=None):
             "algorithmic_work_per_launch": workload.work, "work_unit": "bytes" if workload.bound == "hbm" else "flop",
             "traffic_bytes_per_launch": traffic.get(workload.kernel), "dtype": workload.label,
             "config": workload.config, "validation": validation})
+        if workload.row in roofline.ISSUED_CEILINGS:  # the instruction this build issues is slower than the datasheet's
+            ceiling, ceiling_basis = roofline.ISSUED_CEILINGS[workload.row]
+            rows[-1].update(issued_instruction_ceiling=ceiling, issued_instruction_basis=ceiling_basis,
+                            frac_of_issued_ceiling=achieved / ceiling)
 
     headline = [r for r in rows if r["in_headline"]] or rows
     value = 100.0 * sum(r["frac"] for r in headline) / len(headline)
@@ -441,7 +506,8 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": ",".join(dict.fromkeys(r["dtype"] for r in headline)),
         "data": "synthetic, seeded, resident in HBM: uniform fp32 copy source; N(0,1) BF16/FP16/FP64 GEMM "
-                "operands; exact FP8/INT8/MXFP4 GEMM sets; exact lattices for the resident tiles",
+                "operands; exact FP8/INT8/MXFP4 GEMM sets; exact lattices for the resident tiles; vector chain "
+                "states x0 ~ U[0.5, 1) (INT8: [-4, 4])",
         "config": {"workload": "mean over " + " + ".join(r["name"] for r in headline)
                    + ("; also reported: " + ", ".join(r["name"] for r in rows if not r["in_headline"])
                       if any(not r["in_headline"] for r in rows) else ""),

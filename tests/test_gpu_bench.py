@@ -36,7 +36,13 @@ def test_bench_prints_one_contract_line(gpu):
     assert "workload" in line["config"] and "model" not in line["config"]
     rows = {row["name"]: row for row in line["rows"]}
     assert set(rows) == {"hbm_copy", "peak_bf16", "gemm_bf16", "gemm_fp16", "gemm_fp8", "gemm_int8", "gemm_fp64",
-                         "gemm_mxfp4", "peak_fp8", "peak_fp8_dense", "peak_mxfp4"}
+                         "gemm_mxfp4", "peak_fp8", "peak_fp8_dense", "peak_mxfp4", "vector_fp32", "vector_fp16",
+                         "vector_bf16", "vector_fp64", "vector_int8"}
+    # The vector rows (the specification's FMA-chain configuration) carry the issue ceiling of the
+    # instruction they run where it is below the datasheet figure.
+    for name in ("vector_fp32", "vector_bf16"):
+        assert 0.5 < rows[name]["frac_of_issued_ceiling"] <= 1.0, rows[name]
+    assert rows["vector_int8"]["unit"] == "TOP/s" and rows["vector_int8"]["bound"] == "valu"
     headline = {name for name, row in rows.items() if row["in_headline"]}
     assert headline == {"hbm_copy", "peak_bf16", "gemm_bf16", "gemm_fp8", "gemm_mxfp4"}
     assert all(name in line["config"]["workload"] for name in rows)
