@@ -42,7 +42,7 @@ class _Library:
 def stand_ins(monkeypatch):
     state = {"timed": 0, "corrupt": False, "listing": list(NATIVE_FP32), "spills": 0}
 
-    def launch(kind, inputs, output, coefficients, iterations, unroll, block):
+    def launch(kind, inputs, output, coefficients, iterations, unroll, block, regime_checked=False):
         assert kind == "fp32", kind
         result = ov.run_chains("fp32", inputs.numpy(), coefficients.numpy(), iterations)
         if state["corrupt"]:
@@ -130,3 +130,36 @@ def test_bf16_dot2_refuses_operands_outside_its_bounded_regime():
         bench_vector.launch_vector("bf16_dot2", infinite, infinite.clone(), ok, 16, 16, 64)
     ceiling, basis = roofline.ISSUED_CEILINGS["vector_bf16"]
     assert ceiling == pytest.approx(256 * 2.4e9 * 256 / 3 / 1e12) and "1.5" in basis
+
+
+def test_bf16_dot2_regime_is_checked_once_outside_the_timed_launches(tmp_path, monkeypatch):
+    """The dot2 operand check reads the operands back to the host, which a graph
+    capture forbids and which would add device work to the timed region: the
+    suite checks each operand set once, for the longest run it makes (the odd
+    iteration probe), and every launch it times skips the check."""
+    calls, launches = [], []
+    real_reason = bv.dot2_regime_reason
+
+    def reason(inputs, coefficients, iterations):
+        calls.append(iterations)
+        return real_reason(inputs, coefficients, iterations)
+
+    def launch(kind, inputs, output, coefficients, iterations, unroll, block, regime_checked=False):
+        launches.append((kind, regime_checked))
+        result = ov.run_chains("bf16", inputs.float().numpy(), coefficients.float().numpy(), iterations)
+        output.copy_(torch.from_numpy(np.asarray(result)).to(output.dtype))
+
+    monkeypatch.setattr(bv, "get_device", lambda args: "cpu")
+    monkeypatch.setattr(bv, "available_memory_bytes", lambda: None)
+    monkeypatch.setattr(bv._native, "load", lambda: _Library())
+    monkeypatch.setattr(bv, "dot2_regime_reason", reason)
+    monkeypatch.setattr(bv, "launch_vector", launch)
+    monkeypatch.setattr(bv, "measure", lambda fn, args: (fn(), {"median_ms": 2.0, "min_ms": 1.0,
+                                                                "timing_method": "stand-in"})[1])
+    monkeypatch.setattr(bv.audit, "instructions", lambda kernel: ["v_dot2_f32_bf16 v0, v1, v2, v0"])
+    monkeypatch.setattr(bv.audit, "resources", lambda kernel: {"registers_per_thread": 32, "register_spills": 0})
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *args, **kwargs: None)
+    bv.run_benchmark(_args(tmp_path, "bf16"), {"sm_count": 1})
+    dot2 = [checked for kind, checked in launches if kind == "bf16_dot2"]
+    assert dot2 and all(dot2), launches
+    assert calls == [9]  # --iterations 8, plus the odd-iteration probe

@@ -180,11 +180,24 @@ def dot2_regime_reason(inputs, coefficients, iterations: int) -> str | None:
     return None
 
 
-def launch_vector(kind: str, inputs, output, coefficients, iterations: int, unroll: int, block_threads: int):
-    if kind == "bf16_dot2":
-        reason = dot2_regime_reason(inputs, coefficients, iterations)
-        if reason:
-            raise ValueError(f"BF16 dot2 chains need bounded operands ({reason}); use the bf16_fma variant")
+def require_dot2_regime(inputs, coefficients, iterations: int) -> None:
+    """Raises unless the BF16 dot2 chains may run these operands for this many iterations."""
+    reason = dot2_regime_reason(inputs, coefficients, iterations)
+    if reason:
+        raise ValueError(f"BF16 dot2 chains need bounded operands ({reason}); use the bf16_fma variant")
+
+
+def launch_vector(kind: str, inputs, output, coefficients, iterations: int, unroll: int, block_threads: int,
+                  regime_checked: bool = False):
+    """One launch of the chain kernel on the current stream.
+
+    The dot2 variant's operand check reads the operands back to the host, so
+    a caller that times launches (or captures them in a graph) runs
+    require_dot2_regime once, for at least this many iterations, and passes
+    regime_checked=True.
+    """
+    if kind == "bf16_dot2" and not regime_checked:
+        require_dot2_regime(inputs, coefficients, iterations)
     elements = inputs.shape[1]
     size = inputs.numel() * inputs.element_size()
     _native.call("mb_vector_chains", KINDS[kind], inputs.data_ptr(), output.data_ptr(), coefficients.data_ptr(),
@@ -376,6 +389,12 @@ def run_benchmark(args, metadata):
                     raise SystemExit(f"Vector input/output need {required / 2**30:.2f} GiB; reduce the sweep")
                 inputs, coefficients = make_inputs(dtype, elements, device, args.inputs, args.seed)
                 output = torch.empty_like(inputs)
+                if kind == "bf16_dot2":  # once per operand set, outside every timed launch
+                    reason = dot2_regime_reason(inputs, coefficients, args.iterations + 1)
+                    if reason:
+                        excluded.append({"status": "unsupported", "reason": f"dot2 operand regime: {reason}",
+                                         "variant": suffix})
+                        continue
                 for unroll in args.unroll:
                     if args.iterations % unroll:
                         continue
@@ -384,7 +403,8 @@ def run_benchmark(args, metadata):
 
                     def run(iterations=args.iterations, unroll_value=unroll, kind=kind, inputs=inputs,
                             output=output, coefficients=coefficients, block=block):
-                        launch_vector(kind, inputs, output, coefficients, iterations, unroll_value, block)
+                        launch_vector(kind, inputs, output, coefficients, iterations, unroll_value, block,
+                                      regime_checked=True)
 
                     run()
                     torch.cuda.synchronize()
