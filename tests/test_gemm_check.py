@@ -192,3 +192,38 @@ def test_mx_scale_blocks_layout():
     # One K step (block b) of rows r0..r0+n-1 is one contiguous run of 8*n bytes.
     flat = blocks.reshape(-1)
     assert flat[(1 * rows + 2) * 8:(1 * rows + 4) * 8].tolist() == blocks[1, 2:4].reshape(-1).tolist()
+
+
+def test_crosscheck_bf16_library_c_is_held_to_one_bf16_ulp_of_the_exact_c():
+    """The MXFP4 cross-check compares the library's BF16 C with the suite's exact FP32 C, entry by entry.
+
+    One BF16 ulp of an exact value x = m * 2^e (0.5 <= |m| < 1) is 2^(e-8): 2 for 257 (values in [256, 512)
+    are spaced by 2), 4 for 1000.25. Known answers: round-to-nearest and truncation both stay within one ulp;
+    1008 for 1000.25 is 1.94 ulps off and fails; a nonzero entry where the exact C is 0 fails.
+    """
+    import math
+
+    from triton_chip_benchmarks_amd import crosscheck
+
+    exact = torch.tensor([0.0, 1.0, 3.0, 257.0, 1000.25, -5500.0, 0.75], dtype=torch.float32)
+    assert [math.ldexp(1.0, math.frexp(x)[1] - 8) for x in (257.0, 1000.25)] == [2.0, 4.0]
+    nearest = exact.to(torch.bfloat16)
+    fields = crosscheck._agreement("fp4", nearest, exact, torch)
+    assert fields["library_output"] == "bf16" and fields["elementwise_within_one_bf16_ulp"]
+    assert fields["max_bf16_ulps"] <= 0.5
+    truncated = (exact.view(torch.int32) & ~0xFFFF).view(torch.float32).to(torch.bfloat16)
+    fields = crosscheck._agreement("fp4", truncated, exact, torch)
+    assert fields["elementwise_within_one_bf16_ulp"] and 0.5 < fields["max_bf16_ulps"] < 1.0
+    planted = nearest.clone()
+    planted[4] = 1004.0                                          # 3.75 off: within one ulp of 4
+    assert crosscheck._agreement("fp4", planted, exact, torch)["elementwise_within_one_bf16_ulp"]
+    planted[4] = 1008.0                                          # 7.75 off: 1.94 ulps
+    fields = crosscheck._agreement("fp4", planted, exact, torch)
+    assert not fields["elementwise_within_one_bf16_ulp"] and fields["max_bf16_ulps"] == pytest.approx(7.75 / 4)
+    planted = nearest.clone()
+    planted[0] = 2.0**-20                                        # the exact C is 0 there
+    assert not crosscheck._agreement("fp4", planted, exact, torch)["elementwise_within_one_bf16_ulp"]
+    same = crosscheck._agreement("fp8", exact.clone(), exact, torch)
+    assert same == {"normwise_difference": 0.0}
+    rounded_sums = crosscheck._agreement("bf16", nearest, exact, torch)    # BF16 operands: normwise only
+    assert set(rounded_sums) == {"normwise_difference"}

@@ -6,6 +6,9 @@ same work runs a second way on the same card, with each output checked
 against the other:
   copy   mb_copy (the suite's kernel)  vs  dst.copy_(src) (hipMemcpy device-to-device)
   GEMM   mb_gemm (the suite's kernel)  vs  torch.matmul / torch._scaled_mm / torch._int_mm (hipBLASLt)
+The MXFP4 GEMM runs at BASELINE's 16384^3 and the others at 8192^3. torch's
+MXFP4 path writes a BF16 C only, so its output is checked elementwise against
+the suite's exact FP32 C to within one BF16 unit in the last place.
 This follows the reference's practice of comparing its Triton suite with an
 independent Ascend C implementation on the same chip (ascendc/RESULTS.md:57-108):
 a large gap points at a kernel, not at the silicon. Rates use the suite's
@@ -29,6 +32,7 @@ else:
 
 COPY_SHAPE = {"block_threads": 64, "vectors_per_thread": 1, "policy": "stream"}
 GEMM_SIZE = 8192
+FP4_GEMM_SIZE = 16384
 
 
 def _torch():
@@ -80,14 +84,45 @@ def _library_gemm(dtype, a, b, torch):
     if dtype == "int8" and hasattr(torch, "_int_mm"):
         bt = b.t()
         return lambda: torch._int_mm(a, bt)
+    if dtype == "fp4" and hasattr(torch, "float4_e2m1fn_x2") and hasattr(torch, "float8_e8m0fnu"):
+        # Packed E2M1 pairs, even K in the low nibble, with one E8M0 scale per 32 K elements. The suite's
+        # operands carry unit scales (127) only, so the library's scale layout cannot change the product.
+        m, n, k = a.shape[0], b.shape[0], 2 * a.shape[1]
+        a4, bt4 = a.view(torch.float4_e2m1fn_x2), b.view(torch.float4_e2m1fn_x2).t()
+        unit = torch.full((), 127, dtype=torch.uint8, device=a.device)
+        scale_a = unit.expand(m, k // 32).contiguous().view(torch.float8_e8m0fnu)
+        scale_b = unit.expand(n, k // 32).contiguous().view(torch.float8_e8m0fnu)
+        return lambda: torch._scaled_mm(a4, bt4, scale_a=scale_a, scale_b=scale_b, out_dtype=torch.bfloat16)
     return None
 
 
-def gemm_rows(args, dtypes, size):
+def _agreement(dtype, theirs, c, torch):
+    """Normwise difference of the two outputs; for a BF16 library C of an exact format, the worst entry in ulps.
+
+    The suite's C is exact for FP8/INT8/MXFP4 operands (gemm.TOLERANCE 0), so a BF16 library C must lie within
+    one BF16 ulp of it, entry by entry: 2^(e-8) for an exact value m * 2^e with 0.5 <= |m| < 1 (8 significant
+    bits). Zeros must match exactly. BF16/FP16 operands give rounded sums on both sides, which only the
+    normwise difference compares.
+    """
+    ref, got = c.double(), theirs.double()
+    scale = ref.abs().max().item() or 1.0
+    fields = {"normwise_difference": (got - ref).abs().max().item() / scale}
+    if gemm.TOLERANCE[dtype] == 0.0 and theirs.dtype == torch.bfloat16 and c.dtype == torch.float32:
+        error = (got - ref).abs()
+        _, exponent = torch.frexp(ref)
+        ulp = torch.where(ref == 0, torch.zeros_like(ref), torch.ldexp(torch.ones_like(ref), exponent - 8))
+        fields["library_output"] = "bf16"
+        fields["max_bf16_ulps"] = (error / ulp.clamp_min(torch.finfo(torch.float64).tiny)).max().item()
+        fields["elementwise_within_one_bf16_ulp"] = bool((error <= ulp).all().item())
+    return fields
+
+
+def gemm_rows(args, dtypes, base_size, fp4_size=FP4_GEMM_SIZE):
     """mb_gemm against the torch (hipBLASLt) GEMM on the same operands; outputs cross-checked."""
     torch = _torch()
     rows = []
     for dtype in dtypes:
+        size = fp4_size if dtype == "fp4" else base_size
         a, b, c, scales, a_values, b_values = gemm.gemm_inputs(dtype, size, size, size, "cuda", args.seed)
         del a_values, b_values
         config = max(_native.gemm_configs(dtype), key=lambda cfg: cfg["tile_m"] * cfg["tile_n"])
@@ -105,15 +140,17 @@ def gemm_rows(args, dtypes, size):
             library, reason = None, f"torch library path unavailable: {exc}".splitlines()[0]
         else:
             reason = None if library is not None else "torch has no library GEMM for this format"
-        agreement = None
+        agreement = {"normwise_difference": None}
         if library is not None:
-            ref, got = theirs.double(), c.double()
-            scale = ref.abs().max().item() or 1.0
-            agreement = (got - ref).abs().max().item() / scale
-            tolerance = gemm.TOLERANCE[dtype] or 0.0
-            if agreement > max(tolerance, 1e-6 if dtype in ("fp8", "int8") else tolerance):
-                raise AssertionError(f"{dtype}: mb_gemm and the library disagree (normwise {agreement:.3g})")
-            del theirs, ref, got
+            agreement = _agreement(dtype, theirs, c, torch)
+            normwise = agreement["normwise_difference"]
+            if "elementwise_within_one_bf16_ulp" in agreement:
+                if not agreement["elementwise_within_one_bf16_ulp"]:
+                    raise AssertionError(f"{dtype}: the library's BF16 C is {agreement['max_bf16_ulps']:.3g} BF16 "
+                                         "ulps from mb_gemm's exact C (one allowed)")
+            elif normwise > max(gemm.TOLERANCE[dtype], 1e-6 if dtype in ("fp8", "int8") else 0.0):
+                raise AssertionError(f"{dtype}: mb_gemm and the library disagree (normwise {normwise:.3g})")
+            del theirs
         for name, run in (("mb_gemm", ours), ("torch/hipBLASLt", library)):
             if run is None:
                 rows.append({"check": "gemm", "path": name, "dtype": dtype, "m": size, "n": size, "k": size,
@@ -125,7 +162,7 @@ def gemm_rows(args, dtypes, size):
                          "kernel": _native.gemm_kernel_name(dtype, config) if name == "mb_gemm" else "library",
                          "peak_teraops_per_second": peak,
                          "median_teraops_per_second": 2 * size**3 / (timing["median_ms"] * 1e9),
-                         "fraction_of_peak": peak / peak_value, "normwise_difference": agreement, **timing})
+                         "fraction_of_peak": peak / peak_value, **agreement, **timing})
         del a, b, c, scales
         torch.cuda.empty_cache()
     return rows
@@ -134,9 +171,11 @@ def gemm_rows(args, dtypes, size):
 def build_parser():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--copy-mib", type=int, nargs="+", default=[1024, 2048], help="copy buffer sizes (MiB)")
-    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8"],
-                        choices=["bf16", "fp16", "fp8", "int8"])
+    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8", "fp4"],
+                        choices=["bf16", "fp16", "fp8", "int8", "fp4"])
     parser.add_argument("--gemm-size", type=int, default=GEMM_SIZE, help="square GEMM size (default 8192)")
+    parser.add_argument("--fp4-size", type=int, default=FP4_GEMM_SIZE,
+                        help="square MXFP4 GEMM size (default 16384, BASELINE's configuration)")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--quick", action="store_true", help="small sizes: a smoke check, not a measurement")
     add_common_arguments(parser)
@@ -146,9 +185,9 @@ def build_parser():
 def main(argv=None) -> int:
     args = build_parser().parse_args(argv)
     if args.quick:
-        args.copy_mib, args.gemm_size, args.warmup, args.rep, args.rounds = [8], 512, 5, 10, 3
+        args.copy_mib, args.gemm_size, args.fp4_size, args.warmup, args.rep, args.rounds = [8], 512, 512, 5, 10, 3
     metadata = setup_device(args)
-    rows = copy_rows(args, args.copy_mib) + gemm_rows(args, args.gemm_dtypes, args.gemm_size)
+    rows = copy_rows(args, args.copy_mib) + gemm_rows(args, args.gemm_dtypes, args.gemm_size, args.fp4_size)
     print(f"{'check':6s} {'path':18s} {'case':14s} {'peak':>12s} {'median':>12s} {'% peak':>7s}  note")
     for row in rows:
         if row.get("status") == "unavailable":
@@ -164,6 +203,8 @@ def main(argv=None) -> int:
                 row["median_teraops_per_second"], row["fraction_of_peak"]
             note = "TFLOP/s" + (f", normwise diff {row['normwise_difference']:.2g}"
                                 if row.get("normwise_difference") is not None else "")
+            if row.get("max_bf16_ulps") is not None:
+                note += f", library BF16 C within {row['max_bf16_ulps']:.2f} ulp"
         print(f"{row['check']:6s} {row['path']:18s} {case:14s} {peak:12.1f} {median:12.1f} {100 * frac:7.1f}  {note}")
     emit_results("crosscheck", metadata, args, rows)
     return 0
