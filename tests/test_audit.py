@@ -118,6 +118,8 @@ def test_registered_names_follow_the_mangled_template_arguments():
         == "gemm_mxfp4_256x256x256"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_11MfmaBf16x16EEEvPKh") \
         == "gemm_bf16_256x256x64"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_120gemm_dma_roll_kernelINS_10MfmaFp8x16EEEvPKh") \
+        == "gemm_fp8_256x256x128"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
     assert audit.registered_name("unrelated_symbol") is None
 
@@ -152,8 +154,8 @@ def test_every_gemm_kernel_uses_its_format_mfma(listing):
     assert gemm
     for name in gemm:
         fmt = FORMAT_OF[name.split("_")[1]]
-        # The staged 256x256 BF16/FP16/INT8 kernels issue the 16x16 form.
-        staged16 = fmt in ("bf16", "fp16", "int8") and "_256x256x" in name and not name.endswith("_checked")
+        # The staged 256x256 BF16/FP16/INT8/FP8 kernels issue the 16x16 form.
+        staged16 = fmt in ("bf16", "fp16", "int8", "fp8") and "_256x256x" in name and not name.endswith("_checked")
         expected = (PEAK_INSTRUCTION_16 if staged16 else PEAK_INSTRUCTION)[fmt]
         result = audit.audit_tensor(audit.instructions(name), fmt)
         assert result["tensor_instruction_types"] == [expected], name
@@ -207,10 +209,10 @@ def test_no_packed_fp32_valu_anywhere():
 @pytest.mark.parametrize("name,instruction,mfmas", [("gemm_bf16_256x256x64", "v_mfma_f32_16x16x32_bf16", 256),
                                                      ("gemm_f16_256x256x64", "v_mfma_f32_16x16x32_f16", 256),
                                                      ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8", 256),
-                                                     ("gemm_fp8_256x256x128", "v_mfma_f32_32x32x64_f8f6f4", 64)])
+                                                     ("gemm_fp8_256x256x128", "v_mfma_f32_16x16x128_f8f6f4", 128)])
 def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfmas):
-    """The A-by-DMA fast path keeps every accumulator in its AGPRs (the 16x16
-    forms through their in-place assembly): the K loop (two 128-byte steps)
+    """The A-by-DMA fast path (FP8 in its rolled form) keeps every accumulator in
+    its AGPRs through the in-place assembly of the 16x16 forms: the K loop (two 128-byte steps)
     issues its MFMAs, 64 fragment reads, 16 B stage writes and 32 buffer loads
     (16 of B into registers, 16 LDS-DMA of A) and nothing else on the vector
     side but the A slot address, with no spills."""

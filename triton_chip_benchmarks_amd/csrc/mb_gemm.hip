@@ -13,11 +13,12 @@
 // timing by the caller).
 //
 // Two kernels:
-//   * gemm_dma_kernel (BF16, FP16, INT8 on 16x16 MFMAs; FP8 on 32x32) and
-//     gemm_staged_kernel (MXFP4): 256x256 tiles when the shape divides the
-//     tile. Four waves, one per SIMD, each owning 128x128 outputs in AGPRs:
-//     64 accumulators of 16x16 (the 16x16 instructions sustain a higher clock
-//     under the power limit) or 16 of 32x32. In the staged kernel operands flow
+//   * gemm_dma_kernel (BF16, FP16, INT8 on 16x16 MFMAs), its rolled form
+//     gemm_dma_roll_kernel (FP8 on 16x16x128 MFMAs) and gemm_staged_kernel
+//     (MXFP4): 256x256 tiles when the shape divides the tile. Four waves, one
+//     per SIMD, each owning 128x128 outputs in AGPRs: 64 accumulators of 16x16
+//     (the 16x16 instructions sustain a higher clock under the power limit)
+//     or, for MXFP4, 16 of 32x32. In the staged kernel operands flow
 //     global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128 bytes of every
 //     row) is loaded two steps ahead into one of two register sets, written to
 //     one of two LDS stages a step ahead, and read back as fragments ahead of
@@ -694,6 +695,185 @@ __global__ void __launch_bounds__(256)
 #endif
 }
 
+// ---- 256x256 kernel, A by LDS DMA, one MFMA per block per step (FP8 16x16) --
+
+// The DMA kernel's tiles, LDS layout, A ring, B stages and load pipeline for
+// an instruction whose K slice is a whole 128-byte step: the 16x16x128 FP8
+// form, 32-byte fragments, 8x8 output blocks of 16x16 per wave. A step is 64
+// MFMAs with no substeps, and one set of 8 A and 8 B fragments (128 VGPRs)
+// is all the wave holds: every fragment register is refilled in place after
+// its last use, which leaves room for the two B staging sets beside the 256
+// accumulator AGPRs. The step's one barrier splits it in halves:
+//   first half:  MFMA (i, 4 + j), i = 0..7, j = 0..3, row by row; reads of
+//                B fragments 0..3 of this step (their previous contents were
+//                last used at the end of the previous step); B stage writes
+//                of step kt+1 and the first half of step kt+3's B loads;
+//   barrier      (publishes step kt+1, ends every read of A slot kt % 3);
+//   second half: MFMA (i, j), i = 0..7, j = 0..3; at its start the reads of
+//                B fragments 4..7 of step kt+1, then A fragment i of step
+//                kt+1 right after MFMA (i, 3), its last use; the A DMAs of
+//                step kt+3 into slot kt % 3, then the rest of its B loads.
+// The next step's first use of each fragment is at least 28 MFMAs after its
+// read. The MFMAs are issued in their in-place form (Op::mma_tied) under the
+// DMA kernel's hazard rules: operands come from LDS reads the compiler waits
+// for, and acc_hazard_fence separates the accumulators' zeroing from the
+// first MFMA and the last MFMA from the epilogue.
+template <class Op>
+__global__ void __launch_bounds__(256)
+    gemm_dma_roll_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
+                         const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
+                         int group_m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, TILES = 8;
+  static_assert(Op::M == 16 && Op::LANE_BYTES == 32 && MfmaGeometry<Op>::K_BYTES == ROWB && !Op::SCALED,
+                "16x16 instructions whose K slice is a whole 128-byte step, 32-byte fragments");
+  using Frag = typename Op::Frag;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * REGION];
+  if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
+
+  int tile_m, tile_n;
+  band_tile(M / BM, N / BM, group_m, tile_m, tile_n);
+  const int m0 = tile_m * BM, n0 = tile_n * BM;
+  const int row_bytes = K * Op::ELEM_BITS / 8;
+  const int k_steps = row_bytes / ROWB, last = k_steps - 1;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BM * row_bytes);
+  // B: load j of a step covers rows 32j .. 32j+31; thread t moves row 32j + t/8, chunk t%8.
+  const int voff = (t >> 3) * row_bytes + (t & 7) * 16;
+  uint8_t* const wb = lds + 3 * REGION + (t >> 3) * ROWB + (((t & 7) ^ ((t >> 4) & 7)) << 4);
+  auto load = [&](i32x4 (&v)[NB], int kt, int j) __attribute__((always_inline)) {
+    v[j] = __builtin_bit_cast(i32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(rb, voff, kt * ROWB + j * 32 * row_bytes, 0));
+  };
+  auto store = [&](const i32x4 (&v)[NB], int s, int j) __attribute__((always_inline)) {
+    *reinterpret_cast<i32x4*>(wb + s * REGION + j * 32 * ROWB) = v[j];
+  };
+  // A: the DMA kernel's mapping (instruction i of wave w moves rows 64w+8i .. +7).
+  const int arow = lane >> 3;
+  const int avoff0 = arow * row_bytes + (((lane & 7) ^ (arow >> 1)) << 4);
+  const int avoff1 = arow * row_bytes + (((lane & 7) ^ ((arow >> 1) | 4)) << 4);
+  const uint32_t lds_base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
+  auto dma_a = [&](int slot, int kt, int i) __attribute__((always_inline)) {
+    const int row = 64 * wave + 8 * i;
+    dma16(ra, (i & 1) ? avoff1 : avoff0, kt * ROWB + row * row_bytes, lds_base + slot * REGION + row * ROWB);
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lrow = lane % 16, lgroup = lane / 16;
+  // Lane group g holds logical chunks 2g and 2g+1 of its row: the lane base,
+  // then XOR 16 for the second piece. Fragments are 16 rows apart, which
+  // leaves the swizzle unchanged.
+  const int sw = ((lrow >> 1) & 7) ^ (lgroup * 2);
+  const uint32_t ra0 = (wm * 128 + lrow) * ROWB + (sw << 4);
+  const uint32_t rb0 = 3 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
+  auto frag = [&](uint32_t base, int region, int f) __attribute__((always_inline)) {
+    const uint8_t* p = lds + base + region + f * 16 * ROWB;
+    const uint8_t* q = lds + (base ^ 16u) + region + f * 16 * ROWB;
+    return __builtin_shufflevector(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(q), 0, 1, 2,
+                                   3, 4, 5, 6, 7);
+  };
+  auto frag_a = [&](int slot, int f) __attribute__((always_inline)) { return frag(ra0, slot * REGION, f); };
+  auto frag_b = [&](int s, int f) __attribute__((always_inline)) { return frag(rb0, s * REGION, f); };
+
+  typename Op::Acc acc[TILES][TILES];
+#pragma unroll
+  for (int i = 0; i < TILES; ++i)
+#pragma unroll
+    for (int j = 0; j < TILES; ++j) acc[i][j] = typename Op::Acc{};
+
+  // Prologue (the DMA kernel's): A of steps 0..2 into slots 0..2, B of steps
+  // 0 and 1 in flight, step 0 written to B stage 0, step 2's B into v0.
+  i32x4 v0[NB], v1[NB];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma_a(p, min(p, last), i);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v1, min(1, last), j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) store(v0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v0, min(2, last), j);
+  lds_barrier();
+
+  // Step 0's A fragments and B fragments 4..7; its B 0..3 are read by the first half.
+  Frag fa[TILES], fb[TILES];
+#pragma unroll
+  for (int f = 0; f < TILES; ++f) fa[f] = frag_a(0, f);
+#pragma unroll
+  for (int f = 4; f < TILES; ++f) fb[f] = frag_b(0, f);
+#pragma unroll
+  for (int i = 0; i < TILES; ++i)
+#pragma unroll
+    for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
+
+  // MFMA slots (one MFMA each, its own scheduling region).
+  //   First half (32 slots): B fragment reads in slots 0, 2, 4, 6; stage
+  //     writes every third slot from 1; the first four B loads every sixth
+  //     from 2, each behind the write that frees its registers.
+  //   Second half (32 slots): B fragment reads in slots 0, 2, 4, 6; A DMAs in
+  //     the odd slots below 16; the last four B loads every fourth slot from
+  //     17, after every DMA of their step (so the in-order waits for them,
+  //     which the stage writes take before the barrier that publishes the
+  //     step, cover the DMAs); A fragment i after slot 4i + 3.
+  int slot = 0;  // A slot of the current step: kt % 3
+  auto step = [&](int kt, int s, i32x4 (&vnext)[NB]) __attribute__((always_inline)) {
+    const int next_slot = slot == 2 ? 0 : slot + 1;
+    static_for<0, 32>([&](auto q_c) __attribute__((always_inline)) {
+      constexpr int q = decltype(q_c)::value, i = q / 4, j = 4 + q % 4;
+      constexpr int rd = q < 8 && q % 2 == 0 ? q / 2 : -1;
+      if constexpr (rd >= 0) fb[rd] = frag_b(s, rd);
+      constexpr int wr = q < 24 && q % 3 == 1 ? q / 3 : -1;
+      if constexpr (wr >= 0) store(vnext, s ^ 1, wr);
+      constexpr int ld = q < 24 && q % 6 == 2 ? q / 6 : -1;
+      if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
+      Op::mma_tied(fa[i], fb[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, 32>([&](auto q_c) __attribute__((always_inline)) {
+      constexpr int q = decltype(q_c)::value, i = q / 4, j = q % 4;
+      constexpr int rd = q < 8 && q % 2 == 0 ? 4 + q / 2 : -1;
+      if constexpr (rd >= 0) fb[rd] = frag_b(s ^ 1, rd);
+      constexpr int dm = q < 16 && q % 2 == 1 ? q / 2 : -1;
+      if constexpr (dm >= 0) dma_a(slot, min(kt + 3, last), dm);
+      constexpr int ld = q >= 17 && (q - 17) % 4 == 0 ? 4 + (q - 17) / 4 : -1;
+      if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
+      Op::mma_tied(fa[i], fb[j], acc[i][j]);
+      if constexpr (j == 3) fa[i] = frag_a(next_slot, i);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    slot = next_slot;
+  };
+  for (int kt = 0; kt < k_steps; kt += 2) {
+    step(kt, 0, v1);
+    step(kt + 1, 1, v0);
+  }
+#pragma unroll
+  for (int i = 0; i < TILES; ++i)
+#pragma unroll
+    for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
+
+#pragma unroll
+  for (int i = 0; i < TILES; ++i)
+#pragma unroll
+    for (int j = 0; j < TILES; ++j)
+#pragma unroll
+      for (int r = 0; r < Op::ACC_REGS; ++r) {
+        const int row = m0 + wm * 128 + i * Op::M + Op::out_row(lane, r);
+        const int col = n0 + wn * 128 + j * Op::N + lrow;
+        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+      }
+#endif
+}
+
 // Launchers size their own grid: one workgroup per output tile of their kernel.
 using GemmLauncher = void (*)(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, void*, int, int, int,
                               int, hipStream_t);
@@ -710,24 +890,28 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
 }
 
 // The 256x256 fast-path kernel of an instruction: the A-by-DMA kernel for the
-// unscaled ones, the register-staged kernel (with its scale ring) for MXFP4.
+// unscaled ones (its rolled form when one instruction takes a whole 128-byte
+// step), the register-staged kernel (with its scale ring) for MXFP4.
+template <class Op>
+constexpr auto fast_kernel_fn() {
+  if constexpr (Op::SCALED)
+    return gemm_staged_kernel<Op>;
+  else if constexpr (MfmaGeometry<Op>::K_BYTES == 128)
+    return gemm_dma_roll_kernel<Op>;
+  else
+    return gemm_dma_kernel<Op>;
+}
+
 template <class Op>
 const void* fast_kernel() {
-  if constexpr (!Op::SCALED)
-    return reinterpret_cast<const void*>(gemm_dma_kernel<Op>);
-  else
-    return reinterpret_cast<const void*>(gemm_staged_kernel<Op>);
+  return reinterpret_cast<const void*>(fast_kernel_fn<Op>());
 }
 
 template <class Op>
 void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m,
                         int n, int k, int group_m, hipStream_t stream) {
-  if constexpr (!Op::SCALED)
-    gemm_dma_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
-        a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
-  else
-    gemm_staged_kernel<Op><<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
-        a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
+  fast_kernel_fn<Op>()<<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
+      a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
 // What a variant's fast launcher needs beyond a shape that divides its tile.
@@ -791,7 +975,7 @@ const GemmVariant kGemmVariants[] = {
                    "gemm_f16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
-    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8, MfmaFp8, 128, 256, 256, 6, "gemm_fp8_256x256x128",
+    MB_GEMM_STAGED(MB_MATRIX_FP8_E4M3, MfmaFp8x16, MfmaFp8, 128, 256, 256, 6, "gemm_fp8_256x256x128",
                    "gemm_fp8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),

@@ -177,6 +177,10 @@ struct MfmaI8x16 {
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
 };
 
+// The FP8 form's builtin is tied by the compiler, but the GEMM's rolled
+// kernel (256 accumulators, every fragment refilled in place) still gets
+// accumulator copies and spills from it; mma_tied keeps the accumulator in
+// place there, under the same hazard rules as above.
 struct MfmaFp8x16 {
   static constexpr int M = 16, N = 16, K = 128, ELEM_BITS = 8, LANE_BYTES = 32, ACC_REGS = 4;
   static constexpr bool SCALED = false;
@@ -185,6 +189,9 @@ struct MfmaFp8x16 {
   using Out = float;
   __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  }
+  __device__ static __forceinline__ void mma_tied(Frag a, Frag b, Acc& c) {
+    asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
   }
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
 };
