@@ -118,7 +118,7 @@ def test_registered_names_follow_the_mangled_template_arguments():
         == "gemm_mxfp4_256x256x256"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_11MfmaBf16x16EEEvPKh") \
         == "gemm_bf16_256x256x64"
-    assert audit.registered_name("_ZN2mb12_GLOBAL__N_120gemm_dma_roll_kernelINS_10MfmaFp8x16EEEvPKh") \
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_10MfmaFp8x16EEEvPKh") \
         == "gemm_fp8_256x256x128"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
     assert audit.registered_name("unrelated_symbol") is None
@@ -211,8 +211,8 @@ def test_no_packed_fp32_valu_anywhere():
                                                      ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8", 256),
                                                      ("gemm_fp8_256x256x128", "v_mfma_f32_16x16x128_f8f6f4", 128)])
 def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfmas):
-    """The A-by-DMA fast path (FP8 in its rolled form) keeps every accumulator in
-    its AGPRs through the in-place assembly of the 16x16 forms: the K loop (two 128-byte steps)
+    """The A-by-DMA fast path keeps every accumulator in its AGPRs through the
+    in-place assembly of the 16x16 forms: the K loop (two 128-byte steps)
     issues its MFMAs, 64 fragment reads, 16 B stage writes and 32 buffer loads
     (16 of B into registers, 16 LDS-DMA of A) and nothing else on the vector
     side but the A slot address, with no spills."""

@@ -29,7 +29,7 @@ _MFMA_FORMAT = {"MfmaBf16": "bf16", "MfmaF16": "f16", "MfmaI8": "i8", "MfmaFp8":
                 "MfmaMxfp4": "mxfp4", "MfmaF32": "f32", "MfmaF64": "f64"}
 _PEAK_RE = re.compile(r"tensor_peak_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
 _GEMM_RE = re.compile(r"gemm_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
-_GEMM_STAGED_RE = re.compile(r"gemm_(?:staged|dma|dma_roll)_kernelINS_\d+(Mfma\w+?)EE")
+_GEMM_STAGED_RE = re.compile(r"gemm_(?:staged|dma)_kernelINS_\d+(Mfma\w+?)EE")
 _ELEM_BITS = {"bf16": 16, "f16": 16, "i8": 8, "fp8": 8, "mxfp4": 4, "f32": 32, "f64": 64}
 _COPY_RE = re.compile(r"copy_kernelI(Dv4_j|j|h)Li(\d+)ELi([012])E")
 _READ_RE = re.compile(r"read_sum_kernelI(f|DF16_|t)Li(\d+)E")

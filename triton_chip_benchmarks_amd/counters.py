@@ -121,7 +121,7 @@ def registered_name(demangled: str) -> str:
     if family == "gemm_kernel":
         fmt, bm, bn, bk, _wm, _wn, checked = args
         return f"gemm_{_MFMA_FORMAT[fmt]}_{bm}x{bn}x{bk}{'_checked' if checked in ('true', '1') else ''}"
-    if family in ("gemm_staged_kernel", "gemm_dma_kernel", "gemm_dma_roll_kernel"):
+    if family in ("gemm_staged_kernel", "gemm_dma_kernel"):
         name = _MFMA_FORMAT[args[0].removesuffix("x16")]
         return f"gemm_{name}_256x256x{128 * 8 // _ELEM_BITS[name]}"
     if family == "copy_kernel":

@@ -13,19 +13,19 @@
 // timing by the caller).
 //
 // Two kernels:
-//   * gemm_dma_kernel (BF16, FP16, INT8 on 16x16 MFMAs), its rolled form
-//     gemm_dma_roll_kernel (FP8 on 16x16x128 MFMAs) and gemm_staged_kernel
-//     (MXFP4): 256x256 tiles when the shape divides the tile. Four waves, one
-//     per SIMD, each owning 128x128 outputs in AGPRs: 64 accumulators of 16x16
-//     (the 16x16 instructions sustain a higher clock under the power limit)
-//     or, for MXFP4, 16 of 32x32. In the staged kernel operands flow
-//     global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128 bytes of every
-//     row) is loaded two steps ahead into one of two register sets, written to
-//     one of two LDS stages a step ahead, and read back as fragments ahead of
-//     the MFMAs that use them. Loads, stage writes and fragment reads are
-//     spread across the step's MFMAs, so no burst of memory instructions
-//     stalls the in-order MFMA issue; one barrier per step. The DMA kernel
-//     moves A straight into LDS with LDS-DMA loads instead.
+//   * gemm_dma_kernel (BF16, FP16, INT8, FP8 on 16x16 MFMAs) and
+//     gemm_staged_kernel (MXFP4): 256x256 tiles when the shape divides the
+//     tile. Four waves, one per SIMD, each owning 128x128 outputs in AGPRs:
+//     64 accumulators of 16x16 (the 16x16 instructions sustain a higher clock
+//     under the power limit) or, for MXFP4, 16 of 32x32. In the staged kernel
+//     operands flow global -> VGPR -> LDS -> VGPR -> MFMA: each K step (128
+//     bytes of every row) is loaded two steps ahead into one of two register
+//     sets, written to one of two LDS stages a step ahead, and read back as
+//     fragments ahead of the MFMAs that use them. Loads, stage writes and
+//     fragment reads are spread across the step's MFMAs, so no burst of
+//     memory instructions stalls the in-order MFMA issue; one barrier per
+//     step. The DMA kernel moves A straight into LDS with LDS-DMA loads
+//     instead.
 //   * gemm_kernel: every other tile and every ragged shape (CHECKED
 //     instantiations bound each load and store), operands staged through a
 //     padded, double-buffered LDS tile with 16-byte loads.
@@ -469,265 +469,69 @@ __global__ void __launch_bounds__(256)
 #endif
 }
 
-// ---- 256x256 kernel, A by LDS DMA (BF16, FP16, INT8 on 16x16; FP8 on 32x32) --
+// ---- 256x256 kernel, A by LDS DMA (BF16, FP16, INT8, FP8 on 16x16) --------
 
 // The staged kernel's shape rules with A moved from global memory into LDS by
 // LDS-DMA loads (buffer_load_dwordx4 ... lds) instead of through registers and
-// ds_write: half the stage writes disappear, and the freed registers
-// double-buffer the MFMA fragments. Instructions whose K slice per substep is
-// 64 bytes of a 128-byte step: the 16x16 BF16/FP16/INT8 forms (16-byte
-// fragments, 8x8 per wave) and the 32x32 FP8 form (32-byte fragments, 4x4).
-//
-// The 16x16 BF16/FP16/INT8 MFMAs are issued in their in-place form (Op::
-// mma_tied): the compiler does not tie these instructions' accumulator input
-// to their output, and at 256 accumulator registers the copies it makes
-// instead spill. The kernel keeps the hazard distances the compiler cannot see
-// for them: operands come straight from LDS reads (whose waits the compiler
-// inserts for any reader), and ordered fences (acc_hazard_fence) separate the
-// accumulators' zeroing from the first MFMA and the last MFMA from the
-// epilogue's reads. Every MFMA is its own scheduling region, so program order
-// is the issue order.
+// ds_write, for the unscaled 16x16 instructions: 8x8 output blocks of 16x16
+// per wave.
 //
 // LDS: a ring of three A slots, then two B stages, each 256 rows x 128 bytes
 // (160 KiB in all), with the staged kernel's XOR swizzle. A DMA writes 1 KiB
 // per instruction, lane l at +16*l, i.e. 8 rows; lane l therefore loads the
-// logical chunk that belongs at its physical position in that row.
+// logical chunk that belongs at its physical position in that row. B moves
+// global -> VGPR (two register sets, two steps ahead) -> one of the stages.
 //
-// Per K step kt (A slot kt % 3, B stage kt & 1):
-//   substep 0: B registers holding step kt+1 are written to B stage s^1, and
-//              reloaded with step kt+3; barrier after it (publishes step kt+1,
-//              and ends every read of A slot kt % 3 and of B stage s^1's
-//              previous step);
-//   substep 1: A of step kt+3 is DMAed into slot kt % 3 (freed by that
-//              barrier), then the rest of step kt+3's B loads.
-// A step's DMAs are issued before its last B loads, so the in-order waits for
-// those loads, which the B stage writes of step kt+2 take before the barrier
-// that publishes step kt+3, also cover the DMAs.
+// Fragments: a lane's fragment is 32 bytes of its row's 128-byte step. FP8
+// (16x16x128) takes it in one instruction, lane group g holding logical
+// chunks 2g and 2g+1; BF16, FP16 and INT8 (16-byte operands, 64-byte K
+// slices) take it in two, lane group g holding chunk g for the first and
+// chunk g + 4 for the second, so each block accumulates K in chunk order. One
+// set of 8 A and 8 B fragments (128 VGPRs) is all the wave holds: every
+// fragment register is refilled in place after its last use, which leaves
+// room for the two B staging sets beside the 256 accumulator AGPRs.
+//
+// Per K step kt (A slot kt % 3, B stage s = kt & 1): 64 block updates, and
+// one barrier that splits them in halves:
+//   first half:  blocks (i, 4 + j), i = 0..7, j = 0..3, row by row; reads of
+//                B fragments 0..3 of this step (their previous contents were
+//                last used at the end of the previous step); B registers
+//                holding step kt+1 written to stage s^1, and the first half
+//                of step kt+3's B loads;
+//   barrier      (publishes step kt+1, and ends every read of A slot kt % 3
+//                and of stage s^1's previous step);
+//   second half: blocks (i, j), i = 0..7, j = 0..3; at its start the reads
+//                of B fragments 4..7 of step kt+1, then A fragment i of step
+//                kt+1 right after block (i, 3), its last use; A of step kt+3
+//                DMAed into slot kt % 3, then the rest of its B loads.
+// The next step's first use of each fragment is at least 28 block updates
+// after its read. A step's DMAs are issued before its last B loads, so the
+// in-order waits for those loads, which the B stage writes of step kt+2 take
+// before the barrier that publishes step kt+3, also cover the DMAs.
+//
+// The MFMAs are issued in their in-place form (Op::mma_tied): the compiler
+// does not tie the 16-byte 16x16 instructions' accumulator input to their
+// output, and at 256 accumulator registers the copies it makes instead (for
+// the FP8 form as well, at this register pressure) spill. The kernel keeps
+// the hazard distances the compiler cannot see: operands come straight from
+// LDS reads (whose waits the compiler inserts for any reader), the two MFMAs
+// of one block update accumulate into exactly the same registers (which the
+// hardware orders), and ordered fences (acc_hazard_fence) separate the
+// accumulators' zeroing from the first MFMA and the last MFMA from the
+// epilogue's reads. Every block update is its own scheduling region, so
+// program order is the issue order.
 template <class Op>
 __global__ void __launch_bounds__(256)
     gemm_dma_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
                     const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
                     int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, KS = 2;
-  constexpr int TILES = 128 / Op::M, PIECES = Op::LANE_BYTES / 16;
-  static_assert(MfmaGeometry<Op>::K_BYTES == 64 && !Op::SCALED &&
-                    ((Op::M == 16 && PIECES == 1) || (Op::M == 32 && PIECES == 2)),
-                "unscaled instructions with a 64-byte K slice: 16x16 with 16-byte or 32x32 with 32-byte fragments");
-  using Frag = typename Op::Frag;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * REGION];
-  if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
-
-  int tile_m, tile_n;
-  band_tile(M / BM, N / BM, group_m, tile_m, tile_n);
-  const int m0 = tile_m * BM, n0 = tile_n * BM;
-  const int row_bytes = K * Op::ELEM_BITS / 8;
-  const int k_steps = row_bytes / ROWB, last = k_steps - 1;
-
-  const int t = threadIdx.x, lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BM * row_bytes);
-  // B: load j of a step covers rows 32j .. 32j+31; thread t moves row 32j + t/8, chunk t%8.
-  const int voff = (t >> 3) * row_bytes + (t & 7) * 16;
-  uint8_t* const wb = lds + 3 * REGION + (t >> 3) * ROWB + (((t & 7) ^ ((t >> 4) & 7)) << 4);
-  auto load = [&](i32x4 (&v)[NB], int kt, int j) __attribute__((always_inline)) {
-    v[j] = __builtin_bit_cast(i32x4,
-                              __builtin_amdgcn_raw_buffer_load_b128(rb, voff, kt * ROWB + j * 32 * row_bytes, 0));
-  };
-  auto store = [&](const i32x4 (&v)[NB], int s, int j) __attribute__((always_inline)) {
-    *reinterpret_cast<i32x4*>(wb + s * REGION + j * 32 * ROWB) = v[j];
-  };
-  // A: wave w DMAs rows 64w .. 64w+63 of a step, instruction i rows 64w+8i ..
-  // +7; lane l is row 64w + 8i + l/8 at physical chunk l%8, whose swizzle is
-  // ((8i + l/8) >> 1) & 7 = (l/8 >> 1) | 4(i & 1).
-  const int arow = lane >> 3;
-  const int avoff0 = arow * row_bytes + (((lane & 7) ^ (arow >> 1)) << 4);
-  const int avoff1 = arow * row_bytes + (((lane & 7) ^ ((arow >> 1) | 4)) << 4);
-  const uint32_t lds_base =
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
-  auto dma_a = [&](int slot, int kt, int i) __attribute__((always_inline)) {
-    const int row = 64 * wave + 8 * i;
-    dma16(ra, (i & 1) ? avoff1 : avoff0, kt * ROWB + row * row_bytes, lds_base + slot * REGION + row * ROWB);
-  };
-
-  const int wm = wave & 1, wn = wave >> 1;
-  const int lrow = lane % Op::M, lgroup = lane / Op::M;
-  // Piece p of a lane's fragment in substep ks is its row's logical chunk
-  // ks*4 + lgroup*PIECES + p: the lane base XOR (ks << 6) XOR (p << 4), since
-  // the first chunk is even when PIECES = 2. Fragments are M rows apart; the
-  // A slot base is added per step, B's stage and fragment offsets are
-  // immediates.
-  const int sw = ((lrow >> 1) & 7) ^ (lgroup * PIECES);
-  const uint32_t ra0 = (wm * 128 + lrow) * ROWB + (sw << 4);
-  const uint32_t rb0 = 3 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
-  auto frag = [&](uint32_t base, int region, int ks, int f) __attribute__((always_inline)) {
-    const uint8_t* p = lds + (base ^ (static_cast<uint32_t>(ks) << 6)) + region + f * Op::M * ROWB;
-    if constexpr (PIECES == 1) {
-      return *reinterpret_cast<const i32x4*>(p);
-    } else {
-      const uint8_t* q = lds + (base ^ (static_cast<uint32_t>(ks) << 6) ^ 16u) + region + f * Op::M * ROWB;
-      return __builtin_shufflevector(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(q), 0, 1,
-                                     2, 3, 4, 5, 6, 7);
-    }
-  };
-  auto frag_a = [&](int slot, int ks, int f) __attribute__((always_inline)) {
-    return frag(ra0, slot * REGION, ks, f);
-  };
-  auto frag_b = [&](int s, int ks, int f) __attribute__((always_inline)) { return frag(rb0, s * REGION, ks, f); };
-  auto mma = [&](const Frag& a, const Frag& b, typename Op::Acc& c) __attribute__((always_inline)) {
-    if constexpr (Op::M == 16)
-      Op::mma_tied(a, b, c);
-    else
-      c = Op::mma(a, b, c, 0, 0);
-  };
-
-  typename Op::Acc acc[TILES][TILES];
-#pragma unroll
-  for (int i = 0; i < TILES; ++i)
-#pragma unroll
-    for (int j = 0; j < TILES; ++j) acc[i][j] = typename Op::Acc{};
-
-  // Prologue: A of steps 0..2 into slots 0..2, B of steps 0 and 1 in flight,
-  // step 0 written to B stage 0 (its load waits also cover the older DMAs),
-  // step 2's B into v0.
-  i32x4 v0[NB], v1[NB];
-#pragma unroll
-  for (int p = 0; p < 3; ++p)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dma_a(p, min(p, last), i);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) load(v0, 0, j);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) load(v1, min(1, last), j);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) store(v0, 0, j);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) load(v0, min(2, last), j);
-  lds_barrier();
-
-  // Fragments are double-buffered by substep (set p = ks: two substeps per
-  // step and two steps per loop trip keep the parity static). The next
-  // substep's reads are spread over the first three quarters of the current
-  // one, so they have landed by the barrier (whose LDS wait then costs
-  // nothing) and by the next substep's first MFMAs.
-  Frag fa[2][TILES], fb[2][TILES];
-#pragma unroll
-  for (int f = 0; f < TILES; ++f) {
-    fa[0][f] = frag_a(0, 0, f);
-    fb[0][f] = frag_b(0, 0, f);
-  }
-  if constexpr (Op::M == 16) {
-#pragma unroll
-    for (int i = 0; i < TILES; ++i)
-#pragma unroll
-      for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
-  }
-
-  // MFMA slots (one MFMA each, its own scheduling region) carry the memory
-  // work in their first three quarters: the next substep's fragment reads; in
-  // substep 0 the B stage writes and the first half of step kt+3's B loads,
-  // each behind the write that frees its registers; in substep 1 the A DMAs
-  // of step kt+3 and then the rest of its B loads. The last quarter is MFMAs
-  // only.
-  //   16x16 (64 slots): a fragment read every third slot of the first 48;
-  //     writes every sixth (from 1), loads every twelfth (from 2); DMAs every
-  //     third of the first 24 (from 1), the second-half loads every sixth from 26.
-  //   32x32 (16 slots): fragment f (two reads) in slot f of the first 8;
-  //     write j in slot j, load j in slot 2j+1; DMA i in slot i, the
-  //     second-half loads in slots 8..11.
-  int slot = 0;  // A slot of the current step: kt % 3
-  auto step = [&](int kt, int s, i32x4 (&vnext)[NB]) __attribute__((always_inline)) {
-    const int next_slot = slot == 2 ? 0 : slot + 1;
-    static_for<0, KS>([&](auto ks_c) __attribute__((always_inline)) {
-      constexpr int ks = decltype(ks_c)::value, p = ks, np = ks ^ 1;
-      const int na = ks == 0 ? slot : next_slot, nb = ks == 0 ? s : s ^ 1;
-      constexpr int nks = ks == 0 ? 1 : 0;
-      static_for<0, TILES * TILES>([&](auto slot_c) __attribute__((always_inline)) {
-        constexpr int q = decltype(slot_c)::value, i = q / TILES, j = q % TILES;
-        constexpr bool w16 = TILES == 8;
-        constexpr int fr = w16 ? (q < 48 && q % 3 == 0 ? q / 3 : -1) : (q < 8 ? q : -1);
-        if constexpr (fr >= 0) {
-          if constexpr (fr < TILES)
-            fa[np][fr] = frag_a(na, nks, fr);
-          else
-            fb[np][fr - TILES] = frag_b(nb, nks, fr - TILES);
-        }
-        constexpr int wr = ks != 0 ? -1 : w16 ? (q < 48 && q % 6 == 1 ? q / 6 : -1) : (q < 8 ? q : -1);
-        if constexpr (wr >= 0) store(vnext, s ^ 1, wr);
-        constexpr int ld0 = ks != 0 ? -1 : w16 ? (q < 48 && q % 12 == 2 ? q / 12 : -1)
-                                               : (q < 8 && q % 2 == 1 ? q / 2 : -1);
-        if constexpr (ld0 >= 0) load(vnext, min(kt + 3, last), ld0);
-        constexpr int dm = ks != 1 ? -1 : w16 ? (q < 24 && q % 3 == 1 ? q / 3 : -1) : (q < 8 ? q : -1);
-        if constexpr (dm >= 0) dma_a(slot, min(kt + 3, last), dm);
-        constexpr int ld1 = ks != 1 ? -1 : w16 ? (q >= 26 && q < 48 && (q - 26) % 6 == 0 ? 4 + (q - 26) / 6 : -1)
-                                               : (q >= 8 && q < 12 ? 4 + q - 8 : -1);
-        if constexpr (ld1 >= 0) load(vnext, min(kt + 3, last), ld1);
-        mma(fa[p][i], fb[p][j], acc[i][j]);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-      if constexpr (ks == 0) lds_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    slot = next_slot;
-  };
-  for (int kt = 0; kt < k_steps; kt += 2) {
-    step(kt, 0, v1);
-    step(kt + 1, 1, v0);
-  }
-  if constexpr (Op::M == 16) {
-#pragma unroll
-    for (int i = 0; i < TILES; ++i)
-#pragma unroll
-      for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
-  }
-
-#pragma unroll
-  for (int i = 0; i < TILES; ++i)
-#pragma unroll
-    for (int j = 0; j < TILES; ++j)
-#pragma unroll
-      for (int r = 0; r < Op::ACC_REGS; ++r) {
-        const int row = m0 + wm * 128 + i * Op::M + Op::out_row(lane, r);
-        const int col = n0 + wn * 128 + j * Op::N + lrow;
-        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
-      }
-#endif
-}
-
-// ---- 256x256 kernel, A by LDS DMA, one MFMA per block per step (FP8 16x16) --
-
-// The DMA kernel's tiles, LDS layout, A ring, B stages and load pipeline for
-// an instruction whose K slice is a whole 128-byte step: the 16x16x128 FP8
-// form, 32-byte fragments, 8x8 output blocks of 16x16 per wave. A step is 64
-// MFMAs with no substeps, and one set of 8 A and 8 B fragments (128 VGPRs)
-// is all the wave holds: every fragment register is refilled in place after
-// its last use, which leaves room for the two B staging sets beside the 256
-// accumulator AGPRs. The step's one barrier splits it in halves:
-//   first half:  MFMA (i, 4 + j), i = 0..7, j = 0..3, row by row; reads of
-//                B fragments 0..3 of this step (their previous contents were
-//                last used at the end of the previous step); B stage writes
-//                of step kt+1 and the first half of step kt+3's B loads;
-//   barrier      (publishes step kt+1, ends every read of A slot kt % 3);
-//   second half: MFMA (i, j), i = 0..7, j = 0..3; at its start the reads of
-//                B fragments 4..7 of step kt+1, then A fragment i of step
-//                kt+1 right after MFMA (i, 3), its last use; the A DMAs of
-//                step kt+3 into slot kt % 3, then the rest of its B loads.
-// The next step's first use of each fragment is at least 28 MFMAs after its
-// read. The MFMAs are issued in their in-place form (Op::mma_tied) under the
-// DMA kernel's hazard rules: operands come from LDS reads the compiler waits
-// for, and acc_hazard_fence separates the accumulators' zeroing from the
-// first MFMA and the last MFMA from the epilogue.
-template <class Op>
-__global__ void __launch_bounds__(256)
-    gemm_dma_roll_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
-                         const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
-                         int group_m) {
-#if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, TILES = 8;
-  static_assert(Op::M == 16 && Op::LANE_BYTES == 32 && MfmaGeometry<Op>::K_BYTES == ROWB && !Op::SCALED,
-                "16x16 instructions whose K slice is a whole 128-byte step, 32-byte fragments");
-  using Frag = typename Op::Frag;
+  constexpr int PER_STEP = ROWB / MfmaGeometry<Op>::K_BYTES;  // instructions per block per step
+  static_assert(Op::M == 16 && !Op::SCALED &&
+                    ((PER_STEP == 1 && Op::LANE_BYTES == 32) || (PER_STEP == 2 && Op::LANE_BYTES == 16)),
+                "unscaled 16x16 instructions: one with 32-byte or two with 16-byte operands per 128-byte step");
+  using Frag = i32x8;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * REGION];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
 
@@ -764,17 +568,27 @@ __global__ void __launch_bounds__(256)
 
   const int wm = wave & 1, wn = wave >> 1;
   const int lrow = lane % 16, lgroup = lane / 16;
-  // Lane group g holds logical chunks 2g and 2g+1 of its row: the lane base,
-  // then XOR 16 for the second piece. Fragments are 16 rows apart, which
-  // leaves the swizzle unchanged.
-  const int sw = ((lrow >> 1) & 7) ^ (lgroup * 2);
+  // Lane group g's two pieces: logical chunks 2g and 2g+1 (one instruction,
+  // second piece at XOR 16) or g and g + 4 (two instructions, XOR 64). The
+  // first chunk has the XOR bit clear, so the XOR lands on the swizzled
+  // chunk. Fragments are 16 rows apart, which leaves the swizzle unchanged.
+  constexpr uint32_t second = PER_STEP == 1 ? 16u : 64u;
+  const int sw = ((lrow >> 1) & 7) ^ (lgroup * (PER_STEP == 1 ? 2 : 1));
   const uint32_t ra0 = (wm * 128 + lrow) * ROWB + (sw << 4);
   const uint32_t rb0 = 3 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
   auto frag = [&](uint32_t base, int region, int f) __attribute__((always_inline)) {
     const uint8_t* p = lds + base + region + f * 16 * ROWB;
-    const uint8_t* q = lds + (base ^ 16u) + region + f * 16 * ROWB;
+    const uint8_t* q = lds + (base ^ second) + region + f * 16 * ROWB;
     return __builtin_shufflevector(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(q), 0, 1, 2,
                                    3, 4, 5, 6, 7);
+  };
+  auto mma = [&](const Frag& a, const Frag& b, typename Op::Acc& c) __attribute__((always_inline)) {
+    if constexpr (PER_STEP == 1) {
+      Op::mma_tied(__builtin_bit_cast(typename Op::Frag, a), __builtin_bit_cast(typename Op::Frag, b), c);
+    } else {
+      Op::mma_tied(__builtin_shufflevector(a, a, 0, 1, 2, 3), __builtin_shufflevector(b, b, 0, 1, 2, 3), c);
+      Op::mma_tied(__builtin_shufflevector(a, a, 4, 5, 6, 7), __builtin_shufflevector(b, b, 4, 5, 6, 7), c);
+    }
   };
   auto frag_a = [&](int slot, int f) __attribute__((always_inline)) { return frag(ra0, slot * REGION, f); };
   auto frag_b = [&](int s, int f) __attribute__((always_inline)) { return frag(rb0, s * REGION, f); };
@@ -813,7 +627,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
 
-  // MFMA slots (one MFMA each, its own scheduling region).
+  // Slots (one block update each, its own scheduling region):
   //   First half (32 slots): B fragment reads in slots 0, 2, 4, 6; stage
   //     writes every third slot from 1; the first four B loads every sixth
   //     from 2, each behind the write that frees its registers.
@@ -833,7 +647,7 @@ __global__ void __launch_bounds__(256)
       if constexpr (wr >= 0) store(vnext, s ^ 1, wr);
       constexpr int ld = q < 24 && q % 6 == 2 ? q / 6 : -1;
       if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
-      Op::mma_tied(fa[i], fb[j], acc[i][j]);
+      mma(fa[i], fb[j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     });
     lds_barrier();
@@ -846,7 +660,7 @@ __global__ void __launch_bounds__(256)
       if constexpr (dm >= 0) dma_a(slot, min(kt + 3, last), dm);
       constexpr int ld = q >= 17 && (q - 17) % 4 == 0 ? 4 + (q - 17) / 4 : -1;
       if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
-      Op::mma_tied(fa[i], fb[j], acc[i][j]);
+      mma(fa[i], fb[j], acc[i][j]);
       if constexpr (j == 3) fa[i] = frag_a(next_slot, i);
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -890,14 +704,11 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
 }
 
 // The 256x256 fast-path kernel of an instruction: the A-by-DMA kernel for the
-// unscaled ones (its rolled form when one instruction takes a whole 128-byte
-// step), the register-staged kernel (with its scale ring) for MXFP4.
+// unscaled ones, the register-staged kernel (with its scale ring) for MXFP4.
 template <class Op>
 constexpr auto fast_kernel_fn() {
   if constexpr (Op::SCALED)
     return gemm_staged_kernel<Op>;
-  else if constexpr (MfmaGeometry<Op>::K_BYTES == 128)
-    return gemm_dma_roll_kernel<Op>;
   else
     return gemm_dma_kernel<Op>;
 }
@@ -964,14 +775,14 @@ struct GemmVariant {
               CNAME,                                                                                         \
               reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>),                        \
               GROUP}
-// GROUP: the band height the 8192^3 sweep of 2..32 tile rows measured best per
-// fast-path kernel (INT8 4, FP8 6, the others 8; within about 2% of each other).
+// GROUP: the band height the 8192^3 sweeps measured best per fast-path kernel
+// (BF16 and FP16 4, FP8 6, INT8 7, MXFP4 8).
 const GemmVariant kGemmVariants[] = {
-    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16x16, MfmaBf16, 64, 256, 256, 8, "gemm_bf16_256x256x64",
+    MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16x16, MfmaBf16, 64, 256, 256, 4, "gemm_bf16_256x256x64",
                    "gemm_bf16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 256, 128, 64, 2, 2, "gemm_bf16_256x128x64"),
     MB_GEMM(MB_MATRIX_BF16, MfmaBf16, 128, 128, 64, 2, 2, "gemm_bf16_128x128x64"),
-    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16x16, MfmaF16, 64, 256, 256, 8, "gemm_f16_256x256x64",
+    MB_GEMM_STAGED(MB_MATRIX_F16, MfmaF16x16, MfmaF16, 64, 256, 256, 4, "gemm_f16_256x256x64",
                    "gemm_f16_256x256x64_checked"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 256, 128, 64, 2, 2, "gemm_f16_256x128x64"),
     MB_GEMM(MB_MATRIX_F16, MfmaF16, 128, 128, 64, 2, 2, "gemm_f16_128x128x64"),
@@ -979,7 +790,7 @@ const GemmVariant kGemmVariants[] = {
                    "gemm_fp8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 256, 128, 128, 2, 2, "gemm_fp8_256x128x128"),
     MB_GEMM(MB_MATRIX_FP8_E4M3, MfmaFp8, 128, 128, 128, 2, 2, "gemm_fp8_128x128x128"),
-    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8x16, MfmaI8, 128, 256, 256, 4, "gemm_i8_256x256x128",
+    MB_GEMM_STAGED(MB_MATRIX_I8, MfmaI8x16, MfmaI8, 128, 256, 256, 7, "gemm_i8_256x256x128",
                    "gemm_i8_256x256x128_checked"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 256, 128, 128, 2, 2, "gemm_i8_256x128x128"),
     MB_GEMM(MB_MATRIX_I8, MfmaI8, 128, 128, 128, 2, 2, "gemm_i8_128x128x128"),
