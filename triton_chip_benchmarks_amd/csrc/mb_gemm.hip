@@ -482,11 +482,13 @@ __global__ void __launch_bounds__(256)
 // logical chunk that belongs at its physical position in that row. B moves
 // global -> VGPR (two register sets, two steps ahead) -> one of the stages.
 //
-// Fragments: a lane's fragment is 32 bytes of its row's 128-byte step. FP8
-// (16x16x128) takes it in one instruction, lane group g holding logical
-// chunks 2g and 2g+1; BF16, FP16 and INT8 (16-byte operands, 64-byte K
-// slices) take it in two, lane group g holding chunk g for the first and
-// chunk g + 4 for the second, so each block accumulates K in chunk order. One
+// Fragments: a lane's fragment is 32 bytes of its row's 128-byte step, lane
+// group g (lanes 16g .. 16g+15) holding logical chunks g and g + 4. BF16,
+// FP16 and INT8 (16-byte operands, 64-byte K slices) take it in two
+// instructions, chunks 0..3 and then 4..7, so each block accumulates K in
+// chunk order. FP8 (16x16x128) takes it in one: the instruction's K order is
+// then a permutation of the step's, the same for A and B. Chunks 2g and 2g+1
+// would keep FP8's K order but measured LDS bank conflicts and 1% less. One
 // set of 8 A and 8 B fragments (128 VGPRs) is all the wave holds: every
 // fragment register is refilled in place after its last use, which leaves
 // room for the two B staging sets beside the 256 accumulator AGPRs.
@@ -568,17 +570,16 @@ __global__ void __launch_bounds__(256)
 
   const int wm = wave & 1, wn = wave >> 1;
   const int lrow = lane % 16, lgroup = lane / 16;
-  // Lane group g's two pieces: logical chunks 2g and 2g+1 (one instruction,
-  // second piece at XOR 16) or g and g + 4 (two instructions, XOR 64). The
-  // first chunk has the XOR bit clear, so the XOR lands on the swizzled
-  // chunk. Fragments are 16 rows apart, which leaves the swizzle unchanged.
-  constexpr uint32_t second = PER_STEP == 1 ? 16u : 64u;
-  const int sw = ((lrow >> 1) & 7) ^ (lgroup * (PER_STEP == 1 ? 2 : 1));
+  // Lane group g's two pieces are logical chunks g and g + 4: the swizzled
+  // chunk of the first, then XOR 64 (chunk g has bit 2 clear, so the XOR
+  // lands on the swizzled chunk). Fragments are 16 rows apart, which leaves
+  // the swizzle unchanged.
+  const int sw = ((lrow >> 1) & 7) ^ lgroup;
   const uint32_t ra0 = (wm * 128 + lrow) * ROWB + (sw << 4);
   const uint32_t rb0 = 3 * REGION + (wn * 128 + lrow) * ROWB + (sw << 4);
   auto frag = [&](uint32_t base, int region, int f) __attribute__((always_inline)) {
     const uint8_t* p = lds + base + region + f * 16 * ROWB;
-    const uint8_t* q = lds + (base ^ second) + region + f * 16 * ROWB;
+    const uint8_t* q = lds + (base ^ 64u) + region + f * 16 * ROWB;
     return __builtin_shufflevector(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(q), 0, 1, 2,
                                    3, 4, 5, 6, 7);
   };
