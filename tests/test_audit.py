@@ -228,3 +228,64 @@ def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfm
     # What remains is the per-step A slot address (the ring of three slots is not a power of two).
     assert set(vector) <= {"v_or_b32_e32", "v_lshl_or_b32", "v_add_u32_e32"} and sum(vector.values()) <= 8, vector
     assert summary["timed_loop_other_instructions"]["s_barrier"] == 2
+
+
+def _dma_coverage_violations(body: list[str], horizon: int = 2, trips: int = 4) -> list[tuple[int, int]]:
+    """Simulate gfx9's in-order vmcnt over `trips` passes of a loop body.
+
+    An LDS-DMA issued after barrier e is read after barrier e + horizon, so when
+    the wave reaches that barrier the waits before it must have retired it.
+    Returns (barrier, epoch) for every LDS-DMA still outstanding at a barrier
+    `horizon` or more barriers after its issue, from the second pass on (the
+    first starts empty).
+    """
+    outstanding: list[tuple[bool, int]] = []  # (is LDS-DMA, barriers passed at issue), oldest first
+    passed, violations = 0, []
+    for trip in range(trips):
+        for line in body:
+            name = audit.mnemonic(line)
+            if name.startswith(("buffer_load", "global_load", "buffer_store", "global_store")):
+                outstanding.append((line.rstrip().endswith(" lds"), passed))
+            elif name == "s_waitcnt":
+                match = re.search(r"vmcnt\((\d+)\)", line)
+                if match:
+                    keep = int(match.group(1))
+                    outstanding = outstanding[len(outstanding) - keep:] if keep < len(outstanding) else outstanding
+            elif name == "s_barrier":
+                reaching = passed + 1
+                if trip:
+                    violations += [(reaching, epoch) for dma, epoch in outstanding if dma and epoch <= reaching - horizon]
+                passed = reaching
+    return violations
+
+
+@pytest.mark.parametrize("name", ["gemm_bf16_256x256x64", "gemm_f16_256x256x64", "gemm_i8_256x256x128",
+                                  "gemm_fp8_256x256x128"])
+def test_dma_gemm_loop_waits_cover_every_dma_before_its_reads(listing, name):
+    """The A slots are filled by LDS-DMA issued as inline assembly, which the
+    compiler's wait counts leave out: the kernel relies on the in-order vmcnt
+    waits its B stage writes take for B loads. In the compiled loop, every DMA
+    issued after a step's barrier is retired by the waits before the barrier
+    two steps on, after which the step that reads it begins. Without those
+    waits (a B path that no longer waits on loads, say) DMAs stay in flight,
+    and the check sees it."""
+    assert name in listing
+    body = audit.hot_loop(name)
+    assert sum(line.rstrip().endswith(" lds") for line in body) == 16
+    assert _dma_coverage_violations(body) == []
+    unwaited = [line for line in body if not (audit.mnemonic(line) == "s_waitcnt" and "vmcnt" in line)]
+    assert _dma_coverage_violations(unwaited), "the check must see DMAs left in flight"
+
+
+def test_mxfp4_gemm_loop_waits_cover_every_scale_dma_before_its_reads(listing):
+    """The MXFP4 kernel's scale rows arrive by LDS-DMA three steps ahead: the DMA
+    issued in step kt (after barrier kt-1) is read in step kt+2's last substep,
+    after barrier kt+2, so the waits must retire it within three barriers. Two
+    is too few (the check then reports it), and without the waits it stays in
+    flight."""
+    body = audit.hot_loop("gemm_mxfp4_256x256x256")
+    assert sum(line.rstrip().endswith(" lds") for line in body) == 2
+    assert _dma_coverage_violations(body, horizon=3) == []
+    assert _dma_coverage_violations(body, horizon=2)
+    unwaited = [line for line in body if not (audit.mnemonic(line) == "s_waitcnt" and "vmcnt" in line)]
+    assert _dma_coverage_violations(unwaited, horizon=3)
