@@ -145,7 +145,7 @@ def test_fast_path_over_step_counts(gpu, dtype):
         _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8"])
 def test_band_height_orders_tiles_only(gpu, dtype):
     """group_m orders the tiles and nothing else: every band height, including
     ones taller than the tile rows and values near 2^32 (clamped by mb_gemm),
