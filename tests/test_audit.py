@@ -120,6 +120,8 @@ def test_registered_names_follow_the_mangled_template_arguments():
         == "gemm_bf16_256x256x64"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_115gemm_dma_kernelINS_10MfmaFp8x16EEEvPKh") \
         == "gemm_fp8_256x256x128"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_119gemm_dma_f64_kernelINS_7MfmaF64EEEvPKh") \
+        == "gemm_f64_256x128x16"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
     assert audit.registered_name("unrelated_symbol") is None
 
@@ -259,8 +261,27 @@ def _dma_coverage_violations(body: list[str], horizon: int = 2, trips: int = 4) 
     return violations
 
 
+def test_fp64_dma_gemm_loop_has_no_accumulator_copies(listing):
+    """The 256x128 FP64 fast path: its K loop (two 128-byte steps) issues 256
+    in-place v_mfma_f64_16x16x4_f64, 48 fragment reads (12 per wave per step,
+    two 16-byte pieces each), 8 B stage writes and 24 buffer loads (8 of B, 16
+    LDS-DMA of A), with no spills."""
+    name = "gemm_f64_256x128x16"
+    assert name in listing
+    resources = audit.resources(name)
+    assert resources["register_spills"] == 0 and resources["scratch_bytes"] == 0
+    summary = audit.loop_summary(name)
+    assert summary["timed_loop_matrix_types"] == ["v_mfma_f64_16x16x4_f64"]
+    assert summary["timed_loop_matrix_instructions"] == 256
+    vector = dict(summary["timed_loop_vector_memory_or_alu"])
+    assert {k: vector.pop(k, 0) for k in ("ds_read_b128", "ds_write_b128", "buffer_load_dwordx4")} == \
+        {"ds_read_b128": 48, "ds_write_b128": 8, "buffer_load_dwordx4": 24}
+    assert set(vector) <= {"v_or_b32_e32", "v_lshl_or_b32", "v_add_u32_e32"} and sum(vector.values()) <= 8, vector
+    assert summary["timed_loop_other_instructions"]["s_barrier"] == 2
+
+
 @pytest.mark.parametrize("name", ["gemm_bf16_256x256x64", "gemm_f16_256x256x64", "gemm_i8_256x256x128",
-                                  "gemm_fp8_256x256x128"])
+                                  "gemm_fp8_256x256x128", "gemm_f64_256x128x16"])
 def test_dma_gemm_loop_waits_cover_every_dma_before_its_reads(listing, name):
     """The A slots are filled by LDS-DMA issued as inline assembly, which the
     compiler's wait counts leave out: the kernel relies on the in-order vmcnt

@@ -54,6 +54,8 @@ def registered_name(symbol: str) -> str | None:
     if match:
         fmt = _MFMA_FORMAT[match.group(1).removesuffix("x16")]
         return f"gemm_{fmt}_256x256x{128 * 8 // _ELEM_BITS[fmt]}"
+    if "gemm_dma_f64_kernelI" in symbol:
+        return "gemm_f64_256x128x16"
     match = _COPY_RE.search(symbol)
     if match:
         unit, vpt, policy = match.groups()

@@ -124,6 +124,8 @@ def registered_name(demangled: str) -> str:
     if family in ("gemm_staged_kernel", "gemm_dma_kernel"):
         name = _MFMA_FORMAT[args[0].removesuffix("x16")]
         return f"gemm_{name}_256x256x{128 * 8 // _ELEM_BITS[name]}"
+    if family == "gemm_dma_f64_kernel":
+        return "gemm_f64_256x128x16"
     if family == "copy_kernel":
         unit = "dwordx4" if "__vector(4)" in args[0] else "byte" if "char" in args[0] else "dword"
         policy = {"0": "", "false": "", "1": "_nt", "true": "_nt", "2": "_stream"}[args[2]]

@@ -689,6 +689,188 @@ __global__ void __launch_bounds__(256)
 #endif
 }
 
+// ---- 256x128 kernel, A by LDS DMA (FP64 on 16x16x4) -------------------------
+
+// The DMA kernel's A ring, B stages, swizzle, pipeline and rolled fragments
+// for FP64 on a 256x128 tile: 256 accumulator registers hold 128x64 fp64
+// outputs per wave (8x4 blocks of 16x16, four v_mfma_f64_16x16x4_f64 per
+// block per 128-byte step of 16 doubles). M a multiple of 256, N of 128, K an
+// even number of at least 4 steps.
+//
+// LDS (128 KiB): three A slots of 256 rows and two B stages of 128 rows, 128
+// bytes each. B moves global -> VGPR (two sets of four 16-byte loads per
+// thread, two steps ahead) -> stage.
+//
+// Fragments: lane group g holds logical chunks g and g + 4 of its row, doubles
+// 2g, 2g+1, 8+2g and 9+2g; instruction p of a block takes double p of every
+// lane, the same K permutation for A and B. One set of 8 A and 4 B fragments.
+//
+// Per K step kt (A slot kt % 3, B stage s = kt & 1), 32 block updates and one
+// barrier:
+//   first half:  blocks (i, 2 + j), i = 0..7, j = 0..1, row by row; reads of
+//                B fragments 0..1 of this step; B registers holding step kt+1
+//                written to stage s^1, and two of step kt+3's four B loads;
+//   barrier      (publishes step kt+1, ends every read of A slot kt % 3);
+//   second half: blocks (i, j), j = 0..1; at its start the reads of B
+//                fragments 2..3 of step kt+1, then A fragment i of step kt+1
+//                after block (i, 1); the A DMAs of step kt+3 into slot kt % 3
+//                in the odd slots, then the last two B loads, which the stage
+//                writes of step kt+2 wait for before the barrier that
+//                publishes step kt+3 (so those waits also cover the DMAs).
+template <class Op>
+__global__ void __launch_bounds__(256)
+    gemm_dma_f64_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, const uint8_t* __restrict__,
+                        const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
+                        int group_m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 256, BN = 128, ROWB = 128, AREG = BM * ROWB, BREG = BN * ROWB, NB = 4, TM = 8, TN = 4;
+  static_assert(Op::M == 16 && Op::ELEM_BITS == 64 && Op::LANE_BYTES == 8 && MfmaGeometry<Op>::K_BYTES == 32,
+                "the FP64 16x16x4 instruction: four per block per 128-byte step");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[3 * AREG + 2 * BREG];
+  if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
+
+  int tile_m, tile_n;
+  band_tile(M / BM, N / BN, group_m, tile_m, tile_n);
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int row_bytes = K * Op::ELEM_BITS / 8;
+  const int k_steps = row_bytes / ROWB, last = k_steps - 1;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BN * row_bytes);
+  // B: load j of a step covers rows 32j .. 32j+31; thread t moves row 32j + t/8, chunk t%8.
+  const int voff = (t >> 3) * row_bytes + (t & 7) * 16;
+  uint8_t* const wb = lds + 3 * AREG + (t >> 3) * ROWB + (((t & 7) ^ ((t >> 4) & 7)) << 4);
+  auto load = [&](i32x4 (&v)[NB], int kt, int j) __attribute__((always_inline)) {
+    v[j] = __builtin_bit_cast(i32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(rb, voff, kt * ROWB + j * 32 * row_bytes, 0));
+  };
+  auto store = [&](const i32x4 (&v)[NB], int s, int j) __attribute__((always_inline)) {
+    *reinterpret_cast<i32x4*>(wb + s * BREG + j * 32 * ROWB) = v[j];
+  };
+  // A: the DMA kernel's mapping (instruction i of wave w moves rows 64w+8i .. +7).
+  const int arow = lane >> 3;
+  const int avoff0 = arow * row_bytes + (((lane & 7) ^ (arow >> 1)) << 4);
+  const int avoff1 = arow * row_bytes + (((lane & 7) ^ ((arow >> 1) | 4)) << 4);
+  const uint32_t lds_base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
+  auto dma_a = [&](int slot, int kt, int i) __attribute__((always_inline)) {
+    const int row = 64 * wave + 8 * i;
+    dma16(ra, (i & 1) ? avoff1 : avoff0, kt * ROWB + row * row_bytes, lds_base + slot * AREG + row * ROWB);
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lrow = lane % 16, lgroup = lane / 16;
+  const int sw = ((lrow >> 1) & 7) ^ lgroup;
+  const uint32_t ra0 = (wm * 128 + lrow) * ROWB + (sw << 4);
+  const uint32_t rb0 = 3 * AREG + (wn * 64 + lrow) * ROWB + (sw << 4);
+  auto frag = [&](uint32_t base, int region, int f) __attribute__((always_inline)) {
+    const uint8_t* p = lds + base + region + f * 16 * ROWB;
+    const uint8_t* q = lds + (base ^ 64u) + region + f * 16 * ROWB;
+    return __builtin_shufflevector(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(q), 0, 1, 2,
+                                   3, 4, 5, 6, 7);
+  };
+  auto frag_a = [&](int slot, int f) __attribute__((always_inline)) { return frag(ra0, slot * AREG, f); };
+  auto frag_b = [&](int s, int f) __attribute__((always_inline)) { return frag(rb0, s * BREG, f); };
+  auto mma = [&](const i32x8& a, const i32x8& b, typename Op::Acc& c) __attribute__((always_inline)) {
+    const f64x4 ad = __builtin_bit_cast(f64x4, a), bd = __builtin_bit_cast(f64x4, b);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) Op::mma_tied(ad[p], bd[p], c);
+  };
+
+  typename Op::Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = typename Op::Acc{};
+
+  // Prologue (the DMA kernel's): A of steps 0..2 into slots 0..2, B of steps
+  // 0 and 1 in flight, step 0 written to B stage 0, step 2's B into v0.
+  i32x4 v0[NB], v1[NB];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma_a(p, min(p, last), i);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v1, min(1, last), j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) store(v0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) load(v0, min(2, last), j);
+  lds_barrier();
+
+  i32x8 fa[TM], fb[TN];
+#pragma unroll
+  for (int f = 0; f < TM; ++f) fa[f] = frag_a(0, f);
+#pragma unroll
+  for (int f = 2; f < TN; ++f) fb[f] = frag_b(0, f);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc_hazard_fence(acc[i][j]);
+
+  // Slots (one block update each, its own scheduling region):
+  //   First half (16 slots): B fragment reads in slots 0 and 2; stage writes
+  //     in slots 1, 4, 7, 10; B loads 0 and 1 in slots 2 and 8.
+  //   Second half: B fragment reads in slots 0 and 2; A DMAs in the odd slots;
+  //     B loads 2 and 3 after the last DMA; A fragment i after slot 2i + 1.
+  int slot = 0;  // A slot of the current step: kt % 3
+  auto step = [&](int kt, int s, i32x4 (&vnext)[NB]) __attribute__((always_inline)) {
+    const int next_slot = slot == 2 ? 0 : slot + 1;
+    static_for<0, 16>([&](auto q_c) __attribute__((always_inline)) {
+      constexpr int q = decltype(q_c)::value, i = q / 2, j = 2 + q % 2;
+      constexpr int rd = q < 4 && q % 2 == 0 ? q / 2 : -1;
+      if constexpr (rd >= 0) fb[rd] = frag_b(s, rd);
+      constexpr int wr = q < 12 && q % 3 == 1 ? q / 3 : -1;
+      if constexpr (wr >= 0) store(vnext, s ^ 1, wr);
+      constexpr int ld = q < 12 && q % 6 == 2 ? q / 6 : -1;
+      if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
+      mma(fa[i], fb[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, 16>([&](auto q_c) __attribute__((always_inline)) {
+      constexpr int q = decltype(q_c)::value, i = q / 2, j = q % 2;
+      constexpr int rd = q < 4 && q % 2 == 0 ? 2 + q / 2 : -1;
+      if constexpr (rd >= 0) fb[rd] = frag_b(s ^ 1, rd);
+      constexpr int dm = q % 2 == 1 ? q / 2 : -1;
+      if constexpr (dm >= 0) dma_a(slot, min(kt + 3, last), dm);
+      mma(fa[i], fb[j], acc[i][j]);
+      if constexpr (j == 1) fa[i] = frag_a(next_slot, i);
+      if constexpr (q == 15) {
+        load(vnext, min(kt + 3, last), 2);
+        load(vnext, min(kt + 3, last), 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    slot = next_slot;
+  };
+  for (int kt = 0; kt < k_steps; kt += 2) {
+    step(kt, 0, v1);
+    step(kt + 1, 1, v0);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc_hazard_fence(acc[i][j]);
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < Op::ACC_REGS; ++r) {
+        const int row = m0 + wm * 128 + i * Op::M + Op::out_row(lane, r);
+        const int col = n0 + wn * 64 + j * Op::N + lrow;
+        C[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+      }
+#endif
+}
+
 // Launchers size their own grid: one workgroup per output tile of their kernel.
 using GemmLauncher = void (*)(const uint8_t*, const uint8_t*, const uint8_t*, const uint8_t*, void*, int, int, int,
                               int, hipStream_t);
@@ -704,14 +886,23 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
-// The 256x256 fast-path kernel of an instruction: the A-by-DMA kernel for the
-// unscaled ones, the register-staged kernel (with its scale ring) for MXFP4.
+// The fast-path kernel of an instruction: the A-by-DMA kernel for the unscaled
+// ones (256x256; its 256x128 FP64 form), the register-staged kernel (with its
+// scale ring) for MXFP4.
 template <class Op>
 constexpr auto fast_kernel_fn() {
   if constexpr (Op::SCALED)
     return gemm_staged_kernel<Op>;
+  else if constexpr (Op::ELEM_BITS == 64)
+    return gemm_dma_f64_kernel<Op>;
   else
     return gemm_dma_kernel<Op>;
+}
+
+// Tile width of the fast-path kernel (its height is 256).
+template <class Op>
+constexpr int fast_tile_n() {
+  return Op::ELEM_BITS == 64 ? 128 : 256;
 }
 
 template <class Op>
@@ -722,7 +913,7 @@ const void* fast_kernel() {
 template <class Op>
 void launch_gemm_staged(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c, int m,
                         int n, int k, int group_m, hipStream_t stream) {
-  fast_kernel_fn<Op>()<<<dim3(tile_count(m, n, 256, 256)), dim3(256), 0, stream>>>(
+  fast_kernel_fn<Op>()<<<dim3(tile_count(m, n, 256, fast_tile_n<Op>())), dim3(256), 0, stream>>>(
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
@@ -760,12 +951,12 @@ struct GemmVariant {
               reinterpret_cast<const void*>(gemm_kernel<OP, BM, BN, BK, WM, WN, true>),                      \
               8}
 
-// 256x256 tiles: the staged kernel (BK = 128 bytes of K; instruction SOP) for
-// exact shapes, a checked LDS-staged kernel (tile CM x CN, instruction OP) for
-// the rest.
+// 256x256 tiles (256x128 for FP64): the fast-path kernel (BK = 128 bytes of K;
+// instruction SOP) for exact shapes, a checked LDS-staged kernel (tile CM x CN,
+// instruction OP) for the rest.
 #define MB_GEMM_STAGED(FMT, SOP, OP, BK, CM, CN, GROUP, NAME, CNAME)                                              \
   GemmVariant{FMT,                                                                                           \
-              mb_gemm_config{256, 256, BK, 256},                                                             \
+              mb_gemm_config{256, fast_tile_n<SOP>(), BK, 256},                                              \
               NAME,                                                                                          \
               fast_kernel<SOP>(),                                                                            \
               launch_gemm_staged<SOP>,                                                                       \
@@ -776,8 +967,8 @@ struct GemmVariant {
               CNAME,                                                                                         \
               reinterpret_cast<const void*>(gemm_kernel<OP, CM, CN, BK, 2, 2, true>),                        \
               GROUP}
-// GROUP: the band height the 8192^3 sweeps measured best per fast-path kernel
-// (BF16 and FP16 4, FP8 6, INT8 7, MXFP4 8).
+// GROUP: the band height the sweeps at the benchmark sizes measured best per
+// fast-path kernel (BF16 and FP16 4, FP8 6, INT8 7, MXFP4 8; FP64 flat, 8).
 const GemmVariant kGemmVariants[] = {
     MB_GEMM_STAGED(MB_MATRIX_BF16, MfmaBf16x16, MfmaBf16, 64, 256, 256, 4, "gemm_bf16_256x256x64",
                    "gemm_bf16_256x256x64_checked"),
@@ -799,6 +990,8 @@ const GemmVariant kGemmVariants[] = {
                    "gemm_mxfp4_128x128x256_checked"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 128, 256, 2, 2, "gemm_mxfp4_256x128x256"),
     MB_GEMM(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, "gemm_mxfp4_128x128x256"),
+    MB_GEMM_STAGED(MB_MATRIX_F64, MfmaF64, MfmaF64, 16, 128, 128, 8, "gemm_f64_256x128x16",
+                   "gemm_f64_128x128x16_checked"),
     MB_GEMM(MB_MATRIX_F64, MfmaF64, 128, 128, 16, 2, 2, "gemm_f64_128x128x16"),
     MB_GEMM(MB_MATRIX_F64, MfmaF64, 64, 64, 16, 2, 2, "gemm_f64_64x64x16"),
     MB_GEMM(MB_MATRIX_F32, MfmaF32, 128, 128, 32, 2, 2, "gemm_f32_128x128x32"),

@@ -233,6 +233,11 @@ struct MfmaF64 {
   __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
   }
+  // In-place form for the GEMM's DMA kernel (256 accumulator registers), under
+  // the hazard rules of the 16x16 forms' mma_tied.
+  __device__ static __forceinline__ void mma_tied(Frag a, Frag b, Acc& c) {
+    asm("v_mfma_f64_16x16x4_f64 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
   // The four fp64 results of a lane are strided by 4 rows (measured on gfx950
   // with a row/column-marked product), unlike the 16x16 fp32 forms.
   __device__ static __forceinline__ int out_row(int lane, int r) { return (lane >> 4) + 4 * r; }
