@@ -6,7 +6,8 @@ same work runs a second way on the same card, with each output checked
 against the other:
   copy   mb_copy (the suite's kernel)  vs  dst.copy_(src) (hipMemcpy device-to-device)
   GEMM   mb_gemm (the suite's kernel)  vs  torch.matmul / torch._scaled_mm / torch._int_mm (hipBLASLt)
-The MXFP4 GEMM runs at BASELINE's 16384^3 and the others at 8192^3. torch's
+The MXFP4 GEMM runs at BASELINE's 16384^3, FP64 at its 4096^3 and the others
+at 8192^3. torch's
 MXFP4 path writes a BF16 C only, so its output is checked elementwise against
 the suite's exact FP32 C to within one BF16 unit in the last place.
 This follows the reference's practice of comparing its Triton suite with an
@@ -33,6 +34,7 @@ else:
 COPY_SHAPE = {"block_threads": 64, "vectors_per_thread": 1, "policy": "stream"}
 GEMM_SIZE = 8192
 FP4_GEMM_SIZE = 16384
+FP64_GEMM_SIZE = 4096
 
 
 def _torch():
@@ -74,7 +76,7 @@ def copy_rows(args, sizes_mib):
 
 def _library_gemm(dtype, a, b, torch):
     """The library path for C = A . B^T (B stored [N][K]), or None when torch has none."""
-    if dtype in ("bf16", "fp16"):
+    if dtype in ("bf16", "fp16", "fp64"):
         bt = b.t()
         return lambda: torch.matmul(a, bt)
     if dtype == "fp8" and hasattr(torch, "_scaled_mm"):
@@ -117,12 +119,12 @@ def _agreement(dtype, theirs, c, torch):
     return fields
 
 
-def gemm_rows(args, dtypes, base_size, fp4_size=FP4_GEMM_SIZE):
+def gemm_rows(args, dtypes, base_size, fp4_size=FP4_GEMM_SIZE, fp64_size=FP64_GEMM_SIZE):
     """mb_gemm against the torch (hipBLASLt) GEMM on the same operands; outputs cross-checked."""
     torch = _torch()
     rows = []
     for dtype in dtypes:
-        size = fp4_size if dtype == "fp4" else base_size
+        size = {"fp4": fp4_size, "fp64": fp64_size}.get(dtype, base_size)
         a, b, c, scales, a_values, b_values = gemm.gemm_inputs(dtype, size, size, size, "cuda", args.seed)
         del a_values, b_values
         config = max(_native.gemm_configs(dtype), key=lambda cfg: cfg["tile_m"] * cfg["tile_n"])
@@ -171,11 +173,13 @@ def gemm_rows(args, dtypes, base_size, fp4_size=FP4_GEMM_SIZE):
 def build_parser():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--copy-mib", type=int, nargs="+", default=[1024, 2048], help="copy buffer sizes (MiB)")
-    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8", "fp4"],
-                        choices=["bf16", "fp16", "fp8", "int8", "fp4"])
+    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8", "fp4", "fp64"],
+                        choices=["bf16", "fp16", "fp8", "int8", "fp4", "fp64"])
     parser.add_argument("--gemm-size", type=int, default=GEMM_SIZE, help="square GEMM size (default 8192)")
     parser.add_argument("--fp4-size", type=int, default=FP4_GEMM_SIZE,
                         help="square MXFP4 GEMM size (default 16384, BASELINE's configuration)")
+    parser.add_argument("--fp64-size", type=int, default=FP64_GEMM_SIZE,
+                        help="square FP64 GEMM size (default 4096, BASELINE's configuration)")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--quick", action="store_true", help="small sizes: a smoke check, not a measurement")
     add_common_arguments(parser)
@@ -185,9 +189,11 @@ def build_parser():
 def main(argv=None) -> int:
     args = build_parser().parse_args(argv)
     if args.quick:
-        args.copy_mib, args.gemm_size, args.fp4_size, args.warmup, args.rep, args.rounds = [8], 512, 512, 5, 10, 3
+        args.copy_mib, args.gemm_size, args.fp4_size, args.fp64_size = [8], 512, 512, 512
+        args.warmup, args.rep, args.rounds = 5, 10, 3
     metadata = setup_device(args)
-    rows = copy_rows(args, args.copy_mib) + gemm_rows(args, args.gemm_dtypes, args.gemm_size, args.fp4_size)
+    rows = copy_rows(args, args.copy_mib) + gemm_rows(args, args.gemm_dtypes, args.gemm_size, args.fp4_size,
+                                                      args.fp64_size)
     print(f"{'check':6s} {'path':18s} {'case':14s} {'peak':>12s} {'median':>12s} {'% peak':>7s}  note")
     for row in rows:
         if row.get("status") == "unavailable":
