@@ -178,7 +178,8 @@ const char* mb_gemm_kernel_name(int format, const mb_gemm_config* config);
  * run of 8 bytes per row. K * element bits must be a multiple of 128 (16-byte
  * rows); other shapes are bounded by a checked kernel variant. group_m = 0
  * selects the variant's default band height (tile rows per band: 8, or the
- * measured best of its fast-path kernel: 4 for INT8 and 6 for FP8 256x256);
+ * measured best of its fast-path kernel: 4 for BF16 and FP16, 6 for FP8 and 7
+ * for INT8 256x256);
  * a band taller than the tile rows acts as the full height. The band height
  * orders the tiles only: every value gives the same C.
  * Replaces: bench_tensor.py:172-209 (_gemm_kernel) and 235-246 (_launch),
