@@ -27,7 +27,7 @@ PEAK_INSTRUCTION = {"bf16": "v_mfma_f32_32x32x16_bf16", "fp16": "v_mfma_f32_32x3
 # The _mfma16 peak tiles issue the 16x16 form of the same instruction.
 PEAK_INSTRUCTION_16 = {"bf16": "v_mfma_f32_16x16x32_bf16", "fp16": "v_mfma_f32_16x16x32_f16",
                        "int8": "v_mfma_i32_16x16x64_i8", "fp8": "v_mfma_f32_16x16x128_f8f6f4",
-                       "fp4": "v_mfma_scale_f32_16x16x128_f8f6f4"}
+                       "fp4": "v_mfma_scale_f32_16x16x128_f8f6f4", "fp32": "v_mfma_f32_16x16x4_f32"}
 VECTOR_INSTRUCTION = {"f32": ("fp32", "v_fma_f32"), "f64": ("fp64", "v_fma_f64"), "f16": ("fp16", "v_pk_fma_f16"),
                       "bf16dot": ("bf16", "v_dot2_f32_bf16"), "dot4": ("int8", "v_dot4_i32_i8")}
 
@@ -156,8 +156,8 @@ def test_every_gemm_kernel_uses_its_format_mfma(listing):
     assert gemm
     for name in gemm:
         fmt = FORMAT_OF[name.split("_")[1]]
-        # The staged 256x256 BF16/FP16/INT8/FP8 kernels issue the 16x16 form.
-        staged16 = fmt in ("bf16", "fp16", "int8", "fp8") and "_256x256x" in name and not name.endswith("_checked")
+        # The 256x256 DMA kernels (BF16/FP16/INT8/FP8/FP32) issue the 16x16 form.
+        staged16 = fmt in ("bf16", "fp16", "int8", "fp8", "fp32") and "_256x256x" in name and not name.endswith("_checked")
         expected = (PEAK_INSTRUCTION_16 if staged16 else PEAK_INSTRUCTION)[fmt]
         result = audit.audit_tensor(audit.instructions(name), fmt)
         assert result["tensor_instruction_types"] == [expected], name
@@ -211,6 +211,7 @@ def test_no_packed_fp32_valu_anywhere():
 @pytest.mark.parametrize("name,instruction,mfmas", [("gemm_bf16_256x256x64", "v_mfma_f32_16x16x32_bf16", 256),
                                                      ("gemm_f16_256x256x64", "v_mfma_f32_16x16x32_f16", 256),
                                                      ("gemm_i8_256x256x128", "v_mfma_i32_16x16x64_i8", 256),
+                                                     ("gemm_f32_256x256x32", "v_mfma_f32_16x16x4_f32", 1024),
                                                      ("gemm_fp8_256x256x128", "v_mfma_f32_16x16x128_f8f6f4", 128)])
 def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfmas):
     """The A-by-DMA fast path keeps every accumulator in its AGPRs through the
@@ -281,7 +282,7 @@ def test_fp64_dma_gemm_loop_has_no_accumulator_copies(listing):
 
 
 @pytest.mark.parametrize("name", ["gemm_bf16_256x256x64", "gemm_f16_256x256x64", "gemm_i8_256x256x128",
-                                  "gemm_fp8_256x256x128", "gemm_f64_256x128x16"])
+                                  "gemm_fp8_256x256x128", "gemm_f32_256x256x32", "gemm_f64_256x128x16"])
 def test_dma_gemm_loop_waits_cover_every_dma_before_its_reads(listing, name):
     """The A slots are filled by LDS-DMA issued as inline assembly, which the
     compiler's wait counts leave out: the kernel relies on the in-order vmcnt

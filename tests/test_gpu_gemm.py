@@ -125,7 +125,7 @@ def test_gemm_matches_oracle_every_tile_and_ragged_shapes(gpu, dtype):
             _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8", "fp64"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8", "fp32", "fp64"])
 def test_fast_path_over_step_counts(gpu, dtype):
     """The fast path (256x256; 256x128 for FP64; A through a three-slot LDS ring,
     B through registers) at K step counts 4, 6, 10, 12 and 14, which wrap the
@@ -135,7 +135,7 @@ def test_fast_path_over_step_counts(gpu, dtype):
 
     rng = np.random.default_rng(23)
     config = max(_configs(dtype), key=lambda c: c["tile_m"] * c["tile_n"])
-    elements_per_step = 128 * 8 // {"bf16": 16, "fp16": 16, "int8": 8, "fp8": 8, "fp64": 64}[dtype]
+    elements_per_step = 128 * 8 // {"bf16": 16, "fp16": 16, "int8": 8, "fp8": 8, "fp32": 32, "fp64": 64}[dtype]
     for steps in (4, 6, 10, 12, 14):
         m, n, k = 512, 768, steps * elements_per_step
         launched = _native.gemm_launched_kernel(dtype, config, m, n, k)
@@ -145,7 +145,7 @@ def test_fast_path_over_step_counts(gpu, dtype):
         _assert_matches(dtype, got, ot.gemm_reference(a_values, b_values.T))
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8", "fp64"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8", "fp32", "fp64"])
 def test_band_height_orders_tiles_only(gpu, dtype):
     """group_m orders the tiles and nothing else: every band height, including
     ones taller than the tile rows and values near 2^32 (clamped by mb_gemm),

@@ -76,7 +76,7 @@ def copy_rows(args, sizes_mib):
 
 def _library_gemm(dtype, a, b, torch):
     """The library path for C = A . B^T (B stored [N][K]), or None when torch has none."""
-    if dtype in ("bf16", "fp16", "fp64"):
+    if dtype in ("bf16", "fp16", "fp32", "fp64"):
         bt = b.t()
         return lambda: torch.matmul(a, bt)
     if dtype == "fp8" and hasattr(torch, "_scaled_mm"):
@@ -173,8 +173,8 @@ def gemm_rows(args, dtypes, base_size, fp4_size=FP4_GEMM_SIZE, fp64_size=FP64_GE
 def build_parser():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--copy-mib", type=int, nargs="+", default=[1024, 2048], help="copy buffer sizes (MiB)")
-    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8", "fp4", "fp64"],
-                        choices=["bf16", "fp16", "fp8", "int8", "fp4", "fp64"])
+    parser.add_argument("--gemm-dtypes", nargs="+", default=["bf16", "fp16", "fp8", "int8", "fp4", "fp64", "fp32"],
+                        choices=["bf16", "fp16", "fp8", "int8", "fp4", "fp64", "fp32"])
     parser.add_argument("--gemm-size", type=int, default=GEMM_SIZE, help="square GEMM size (default 8192)")
     parser.add_argument("--fp4-size", type=int, default=FP4_GEMM_SIZE,
                         help="square MXFP4 GEMM size (default 16384, BASELINE's configuration)")

@@ -531,8 +531,10 @@ __global__ void __launch_bounds__(256)
   constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, TILES = 8;
   constexpr int PER_STEP = ROWB / MfmaGeometry<Op>::K_BYTES;  // instructions per block per step
   static_assert(Op::M == 16 && !Op::SCALED &&
-                    ((PER_STEP == 1 && Op::LANE_BYTES == 32) || (PER_STEP == 2 && Op::LANE_BYTES == 16)),
-                "unscaled 16x16 instructions: one with 32-byte or two with 16-byte operands per 128-byte step");
+                    ((PER_STEP == 1 && Op::LANE_BYTES == 32) || (PER_STEP == 2 && Op::LANE_BYTES == 16) ||
+                     (PER_STEP == 8 && Op::LANE_BYTES == 4)),
+                "unscaled 16x16 instructions: one with 32-byte, two with 16-byte or eight with 4-byte operands "
+                "per 128-byte step");
   using Frag = i32x8;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * REGION];
   if (K < 0) lds[threadIdx.x] = 0;  // keeps DMA-written reads live; never executed
@@ -586,9 +588,13 @@ __global__ void __launch_bounds__(256)
   auto mma = [&](const Frag& a, const Frag& b, typename Op::Acc& c) __attribute__((always_inline)) {
     if constexpr (PER_STEP == 1) {
       Op::mma_tied(__builtin_bit_cast(typename Op::Frag, a), __builtin_bit_cast(typename Op::Frag, b), c);
-    } else {
+    } else if constexpr (PER_STEP == 2) {
       Op::mma_tied(__builtin_shufflevector(a, a, 0, 1, 2, 3), __builtin_shufflevector(b, b, 0, 1, 2, 3), c);
       Op::mma_tied(__builtin_shufflevector(a, a, 4, 5, 6, 7), __builtin_shufflevector(b, b, 4, 5, 6, 7), c);
+    } else {
+      const f32x8 af = __builtin_bit_cast(f32x8, a), bf = __builtin_bit_cast(f32x8, b);
+#pragma unroll
+      for (int p = 0; p < 8; ++p) Op::mma_tied(af[p], bf[p], c);
     }
   };
   auto frag_a = [&](int slot, int f) __attribute__((always_inline)) { return frag(ra0, slot * REGION, f); };
@@ -994,6 +1000,8 @@ const GemmVariant kGemmVariants[] = {
                    "gemm_f64_128x128x16_checked"),
     MB_GEMM(MB_MATRIX_F64, MfmaF64, 128, 128, 16, 2, 2, "gemm_f64_128x128x16"),
     MB_GEMM(MB_MATRIX_F64, MfmaF64, 64, 64, 16, 2, 2, "gemm_f64_64x64x16"),
+    MB_GEMM_STAGED(MB_MATRIX_F32, MfmaF32x16, MfmaF32, 32, 128, 128, 8, "gemm_f32_256x256x32",
+                   "gemm_f32_128x128x32_checked"),
     MB_GEMM(MB_MATRIX_F32, MfmaF32, 128, 128, 32, 2, 2, "gemm_f32_128x128x32"),
 };
 

@@ -23,6 +23,7 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -221,6 +222,24 @@ struct MfmaF32 {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
   __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_32(lane, r); }
+};
+
+// v_mfma_f32_16x16x4_f32: one fp32 per lane, IEEE fp32 multiply-accumulate
+// (16x16 tile), for the GEMM's DMA kernel; in place like the 16x16 forms
+// above (mma_tied).
+struct MfmaF32x16 {
+  static constexpr int M = 16, N = 16, K = 4, ELEM_BITS = 32, LANE_BYTES = 4, ACC_REGS = 4;
+  static constexpr bool SCALED = false;
+  using Frag = float;
+  using Acc = f32x4;
+  using Out = float;
+  __device__ static __forceinline__ Acc mma(Frag a, Frag b, Acc c, int, int) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ void mma_tied(Frag a, Frag b, Acc& c) {
+    asm("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+  __device__ static __forceinline__ int out_row(int lane, int r) { return out_row_16(lane, r); }
 };
 
 // v_mfma_f64_16x16x4_f64: one fp64 per lane, fp64 accumulate (16x16 tile).
