@@ -214,11 +214,11 @@ def test_no_packed_fp32_valu_anywhere():
                                                      ("gemm_f32_256x256x32", "v_mfma_f32_16x16x4_f32", 1024),
                                                      ("gemm_fp8_256x256x128", "v_mfma_f32_16x16x128_f8f6f4", 128)])
 def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfmas):
-    """The A-by-DMA fast path keeps every accumulator in its AGPRs through the
+    """The all-DMA fast path keeps every accumulator in its AGPRs through the
     in-place assembly of the 16x16 forms: the K loop (two 128-byte steps)
-    issues its MFMAs, 64 fragment reads, 16 B stage writes and 32 buffer loads
-    (16 of B into registers, 16 LDS-DMA of A) and nothing else on the vector
-    side but the A slot address, with no spills."""
+    issues its MFMAs, 64 fragment reads and 32 LDS-DMA loads (16 of A, 16 of
+    B), no LDS writes, and nothing else on the vector side but the A slot
+    address, with no spills."""
     assert name in listing
     resources = audit.resources(name)
     assert resources["register_spills"] == 0 and resources["scratch_bytes"] == 0
@@ -227,28 +227,34 @@ def test_dma_gemm_loop_has_no_accumulator_copies(listing, name, instruction, mfm
     assert summary["timed_loop_matrix_instructions"] == mfmas
     vector = dict(summary["timed_loop_vector_memory_or_alu"])
     assert {k: vector.pop(k, 0) for k in ("ds_read_b128", "ds_write_b128", "buffer_load_dwordx4")} == \
-        {"ds_read_b128": 64, "ds_write_b128": 16, "buffer_load_dwordx4": 32}
+        {"ds_read_b128": 64, "ds_write_b128": 0, "buffer_load_dwordx4": 32}
+    assert sum(line.rstrip().endswith(" lds") for line in audit.hot_loop(name)) == 32
     # What remains is the per-step A slot address (the ring of three slots is not a power of two).
-    assert set(vector) <= {"v_or_b32_e32", "v_lshl_or_b32", "v_add_u32_e32"} and sum(vector.values()) <= 8, vector
+    assert set(vector) <= {"v_or_b32_e32", "v_lshl_or_b32", "v_add_u32_e32", "v_readfirstlane_b32"} and \
+        sum(vector.values()) <= 16, vector
     assert summary["timed_loop_other_instructions"]["s_barrier"] == 2
 
 
-def _dma_coverage_violations(body: list[str], horizon: int = 2, trips: int = 4) -> list[tuple[int, int]]:
+def _dma_coverage_violations(body: list[str], horizon=2, trips: int = 4) -> list[tuple[int, int]]:
     """Simulate gfx9's in-order vmcnt over `trips` passes of a loop body.
 
     An LDS-DMA issued after barrier e is read after barrier e + horizon, so when
     the wave reaches that barrier the waits before it must have retired it.
-    Returns (barrier, epoch) for every LDS-DMA still outstanding at a barrier
-    `horizon` or more barriers after its issue, from the second pass on (the
-    first starts empty).
+    `horizon` is a number, or a function of the DMA's ordinal among the DMAs
+    issued since the last barrier. Returns (barrier, epoch) for every LDS-DMA
+    still outstanding at a barrier its horizon or more barriers after its
+    issue, from the second pass on (the first starts empty).
     """
-    outstanding: list[tuple[bool, int]] = []  # (is LDS-DMA, barriers passed at issue), oldest first
-    passed, violations = 0, []
+    horizon_of = horizon if callable(horizon) else (lambda ordinal: horizon)
+    outstanding: list[tuple[int | None, int]] = []  # (horizon of an LDS-DMA, barriers passed at issue), oldest first
+    passed, violations, ordinal = 0, [], 0
     for trip in range(trips):
         for line in body:
             name = audit.mnemonic(line)
             if name.startswith(("buffer_load", "global_load", "buffer_store", "global_store")):
-                outstanding.append((line.rstrip().endswith(" lds"), passed))
+                dma = line.rstrip().endswith(" lds")
+                outstanding.append((horizon_of(ordinal) if dma else None, passed))
+                ordinal += dma
             elif name == "s_waitcnt":
                 match = re.search(r"vmcnt\((\d+)\)", line)
                 if match:
@@ -257,8 +263,8 @@ def _dma_coverage_violations(body: list[str], horizon: int = 2, trips: int = 4) 
             elif name == "s_barrier":
                 reaching = passed + 1
                 if trip:
-                    violations += [(reaching, epoch) for dma, epoch in outstanding if dma and epoch <= reaching - horizon]
-                passed = reaching
+                    violations += [(reaching, epoch) for h, epoch in outstanding if h and epoch <= reaching - h]
+                passed, ordinal = reaching, 0
     return violations
 
 
@@ -282,15 +288,34 @@ def test_fp64_dma_gemm_loop_has_no_accumulator_copies(listing):
 
 
 @pytest.mark.parametrize("name", ["gemm_bf16_256x256x64", "gemm_f16_256x256x64", "gemm_i8_256x256x128",
-                                  "gemm_fp8_256x256x128", "gemm_f32_256x256x32", "gemm_f64_256x128x16"])
-def test_dma_gemm_loop_waits_cover_every_dma_before_its_reads(listing, name):
-    """The A slots are filled by LDS-DMA issued as inline assembly, which the
-    compiler's wait counts leave out: the kernel relies on the in-order vmcnt
-    waits its B stage writes take for B loads. In the compiled loop, every DMA
-    issued after a step's barrier is retired by the waits before the barrier
-    two steps on, after which the step that reads it begins. Without those
-    waits (a B path that no longer waits on loads, say) DMAs stay in flight,
-    and the check sees it."""
+                                  "gemm_fp8_256x256x128", "gemm_f32_256x256x32"])
+def test_all_dma_gemm_loop_waits_cover_every_dma_before_its_reads(listing, name):
+    """Both operands arrive by LDS-DMA issued as inline assembly, which the
+    compiler's wait counts leave out: the kernel's own vmcnt(8) before each
+    barrier orders them. After step kt's barrier a wave issues step kt+2's B
+    (read after the next barrier: horizon 1) and then step kt+3's A (read
+    after the barrier two steps on: horizon 2). In the compiled loop the waits
+    retire every DMA within its horizon; giving A's DMAs B's horizon, or taking
+    the waits out, leaves DMAs in flight, and the check sees it."""
+    assert name in listing
+    body = audit.hot_loop(name)
+    assert sum(line.rstrip().endswith(" lds") for line in body) == 32
+    b_then_a = lambda ordinal: 1 if ordinal < 8 else 2  # noqa: E731
+    assert _dma_coverage_violations(body, horizon=b_then_a) == []
+    assert _dma_coverage_violations(body, horizon=1), "A's DMAs are not retired within one barrier"
+    unwaited = [line for line in body if not (audit.mnemonic(line) == "s_waitcnt" and "vmcnt" in line)]
+    assert _dma_coverage_violations(unwaited, horizon=b_then_a), "the check must see DMAs left in flight"
+
+
+def test_fp64_dma_gemm_loop_waits_cover_every_dma_before_its_reads(listing):
+    """The FP64 kernel's A slots are filled by LDS-DMA issued as inline
+    assembly, which the compiler's wait counts leave out: the kernel relies on
+    the in-order vmcnt waits its B stage writes take for B loads. In the
+    compiled loop, every DMA issued after a step's barrier is retired by the
+    waits before the barrier two steps on, after which the step that reads it
+    begins. Without those waits (a B path that no longer waits on loads, say)
+    DMAs stay in flight, and the check sees it."""
+    name = "gemm_f64_256x128x16"
     assert name in listing
     body = audit.hot_loop(name)
     assert sum(line.rstrip().endswith(" lds") for line in body) == 16

@@ -127,10 +127,11 @@ def test_gemm_matches_oracle_every_tile_and_ragged_shapes(gpu, dtype):
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "int8", "fp8", "fp32", "fp64"])
 def test_fast_path_over_step_counts(gpu, dtype):
-    """The fast path (256x256; 256x128 for FP64; A through a three-slot LDS ring,
-    B through registers) at K step counts 4, 6, 10, 12 and 14, which wrap the
-    three-slot ring at every phase, on lattice operands (exact; FP64 on N(0,1)
-    within its tolerance), with M != N so a transposed tile order would show."""
+    """The fast path (256x256 with A and B by LDS-DMA into rings of three and
+    two slots; 256x128 for FP64, B through registers) at K step counts 4, 6,
+    10, 12 and 14, which wrap the three-slot ring at every phase, on lattice
+    operands (exact; FP64 on N(0,1) within its tolerance), with M != N so a
+    transposed tile order would show."""
     from triton_chip_benchmarks_amd import _native
 
     rng = np.random.default_rng(23)

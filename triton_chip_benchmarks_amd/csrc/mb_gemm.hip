@@ -250,6 +250,11 @@ __device__ __forceinline__ void band_tile(int tiles_m, int tiles_n, int group_m,
   tile_n = (pid % band) / rows_in_band;
 }
 
+// s_waitcnt's immediate for vmcnt(n) alone (n < 64): vmcnt's low four bits
+// at 3:0 and high two at 15:14, expcnt (6:4) and lgkmcnt (11:8) at their
+// maxima, which wait for nothing.
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // Barrier that orders LDS only: global loads in flight stay in flight across it.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -469,18 +474,19 @@ __global__ void __launch_bounds__(256)
 #endif
 }
 
-// ---- 256x256 kernel, A by LDS DMA (BF16, FP16, INT8, FP8 on 16x16) --------
+// ---- 256x256 kernel, A and B by LDS DMA (BF16, FP16, INT8, FP8, FP32 on 16x16)
 
-// The staged kernel's shape rules with A moved from global memory into LDS by
-// LDS-DMA loads (buffer_load_dwordx4 ... lds) instead of through registers and
-// ds_write, for the unscaled 16x16 instructions: 8x8 output blocks of 16x16
-// per wave.
+// The staged kernel's shape rules with both operands moved from global memory
+// into LDS by LDS-DMA loads (buffer_load_dwordx4 ... lds) instead of through
+// registers and ds_write, for the unscaled 16x16 instructions: 8x8 output
+// blocks of 16x16 per wave.
 //
-// LDS: a ring of three A slots, then two B stages, each 256 rows x 128 bytes
-// (160 KiB in all), with the staged kernel's XOR swizzle. A DMA writes 1 KiB
-// per instruction, lane l at +16*l, i.e. 8 rows; lane l therefore loads the
-// logical chunk that belongs at its physical position in that row. B moves
-// global -> VGPR (two register sets, two steps ahead) -> one of the stages.
+// LDS: a ring of three A slots, then a ring of two B slots, each 256 rows x
+// 128 bytes (160 KiB in all), with the staged kernel's XOR swizzle. A DMA
+// writes 1 KiB per instruction, lane l at +16*l, i.e. 8 rows; lane l therefore
+// loads the logical chunk that belongs at its physical position in that row.
+// Instruction i of wave w moves rows 64w + 8i .. +7 of its operand's tile, so
+// a wave issues 8 DMAs per operand per step.
 //
 // Fragments: a lane's fragment is 32 bytes of its row's 128-byte step, lane
 // group g (lanes 16g .. 16g+15) holding logical chunks g and g + 4. BF16,
@@ -490,26 +496,26 @@ __global__ void __launch_bounds__(256)
 // then a permutation of the step's, the same for A and B. Chunks 2g and 2g+1
 // would keep FP8's K order but measured LDS bank conflicts and 1% less. One
 // set of 8 A and 8 B fragments (128 VGPRs) is all the wave holds: every
-// fragment register is refilled in place after its last use, which leaves
-// room for the two B staging sets beside the 256 accumulator AGPRs.
+// fragment register is refilled in place after its last use.
 //
-// Per K step kt (A slot kt % 3, B stage s = kt & 1): 64 block updates, and
-// one barrier that splits them in halves:
+// Per K step kt (A slot kt % 3, B slot s = kt & 1): 64 block updates, and
+// one wait and barrier that split them in halves:
 //   first half:  blocks (i, 4 + j), i = 0..7, j = 0..3, row by row; reads of
 //                B fragments 0..3 of this step (their previous contents were
-//                last used at the end of the previous step); B registers
-//                holding step kt+1 written to stage s^1, and the first half
-//                of step kt+3's B loads;
-//   barrier      (publishes step kt+1, and ends every read of A slot kt % 3
-//                and of stage s^1's previous step);
+//                last used at the end of the previous step), and no other
+//                memory traffic;
+//   wait         vmcnt(8): the wave's DMAs in flight are then at most the
+//                last eight it issued, step kt+2's A, so step kt+1's A (issued
+//                two steps back) and B (one step back) are in LDS;
+//   barrier      (publishes step kt+1 from every wave, and ends every read of
+//                A slot kt % 3 and of B slot s);
 //   second half: blocks (i, j), i = 0..7, j = 0..3; at its start the reads
 //                of B fragments 4..7 of step kt+1, then A fragment i of step
-//                kt+1 right after block (i, 3), its last use; A of step kt+3
-//                DMAed into slot kt % 3, then the rest of its B loads.
+//                kt+1 right after block (i, 3), its last use; B of step kt+2
+//                DMAed into slot s, then A of step kt+3 into slot kt % 3.
 // The next step's first use of each fragment is at least 28 block updates
-// after its read. A step's DMAs are issued before its last B loads, so the
-// in-order waits for those loads, which the B stage writes of step kt+2 take
-// before the barrier that publishes step kt+3, also cover the DMAs.
+// after its read. The compiler does not count the DMAs (they are inline
+// assembly), so the one explicit wait is what orders them before their reads.
 //
 // The MFMAs are issued in their in-place form (Op::mma_tied): the compiler
 // does not tie the 16-byte 16x16 instructions' accumulator input to their
@@ -528,7 +534,7 @@ __global__ void __launch_bounds__(256)
                     const uint8_t* __restrict__, typename Op::Out* __restrict__ C, int M, int N, int K,
                     int group_m) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, NB = 8, TILES = 8;
+  constexpr int BM = 256, ROWB = 128, REGION = 256 * ROWB, TILES = 8;
   constexpr int PER_STEP = ROWB / MfmaGeometry<Op>::K_BYTES;  // instructions per block per step
   static_assert(Op::M == 16 && !Op::SCALED &&
                     ((PER_STEP == 1 && Op::LANE_BYTES == 32) || (PER_STEP == 2 && Op::LANE_BYTES == 16) ||
@@ -549,25 +555,16 @@ __global__ void __launch_bounds__(256)
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A + static_cast<int64_t>(m0) * row_bytes, BM * row_bytes);
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B + static_cast<int64_t>(n0) * row_bytes, BM * row_bytes);
-  // B: load j of a step covers rows 32j .. 32j+31; thread t moves row 32j + t/8, chunk t%8.
-  const int voff = (t >> 3) * row_bytes + (t & 7) * 16;
-  uint8_t* const wb = lds + 3 * REGION + (t >> 3) * ROWB + (((t & 7) ^ ((t >> 4) & 7)) << 4);
-  auto load = [&](i32x4 (&v)[NB], int kt, int j) __attribute__((always_inline)) {
-    v[j] = __builtin_bit_cast(i32x4,
-                              __builtin_amdgcn_raw_buffer_load_b128(rb, voff, kt * ROWB + j * 32 * row_bytes, 0));
-  };
-  auto store = [&](const i32x4 (&v)[NB], int s, int j) __attribute__((always_inline)) {
-    *reinterpret_cast<i32x4*>(wb + s * REGION + j * 32 * ROWB) = v[j];
-  };
-  // A: the DMA kernel's mapping (instruction i of wave w moves rows 64w+8i .. +7).
-  const int arow = lane >> 3;
-  const int avoff0 = arow * row_bytes + (((lane & 7) ^ (arow >> 1)) << 4);
-  const int avoff1 = arow * row_bytes + (((lane & 7) ^ ((arow >> 1) | 4)) << 4);
+  // Both operands: instruction i of wave w moves rows 64w+8i .. +7 (lane l row l/8, the chunk stored at
+  // physical chunk l%8 of its row) into LDS region `region`: A slots are regions 0..2, B slots 3 and 4.
+  const int drow = lane >> 3;
+  const int dvoff0 = drow * row_bytes + (((lane & 7) ^ (drow >> 1)) << 4);
+  const int dvoff1 = drow * row_bytes + (((lane & 7) ^ ((drow >> 1) | 4)) << 4);
   const uint32_t lds_base =
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
-  auto dma_a = [&](int slot, int kt, int i) __attribute__((always_inline)) {
+  auto dma = [&](__amdgpu_buffer_rsrc_t r, int region, int kt, int i) __attribute__((always_inline)) {
     const int row = 64 * wave + 8 * i;
-    dma16(ra, (i & 1) ? avoff1 : avoff0, kt * ROWB + row * row_bytes, lds_base + slot * REGION + row * ROWB);
+    dma16(r, (i & 1) ? dvoff1 : dvoff0, kt * ROWB + row * row_bytes, lds_base + region * REGION + row * ROWB);
   };
 
   const int wm = wave & 1, wn = wave >> 1;
@@ -606,21 +603,17 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < TILES; ++j) acc[i][j] = typename Op::Acc{};
 
-  // Prologue (the DMA kernel's): A of steps 0..2 into slots 0..2, B of steps
-  // 0 and 1 in flight, step 0 written to B stage 0, step 2's B into v0.
-  i32x4 v0[NB], v1[NB];
+  // Prologue: A of steps 0..2 into A slots 0..2 and B of steps 0 and 1 into B
+  // slots 0 and 1, all of it in LDS before the barrier.
 #pragma unroll
   for (int p = 0; p < 3; ++p)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dma_a(p, min(p, last), i);
+    for (int i = 0; i < 8; ++i) dma(ra, p, min(p, last), i);
 #pragma unroll
-  for (int j = 0; j < NB; ++j) load(v0, 0, j);
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
-  for (int j = 0; j < NB; ++j) load(v1, min(1, last), j);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) store(v0, 0, j);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) load(v0, min(2, last), j);
+    for (int i = 0; i < 8; ++i) dma(rb, 3 + p, min(p, last), i);
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
   lds_barrier();
 
   // Step 0's A fragments and B fragments 4..7; its B 0..3 are read by the first half.
@@ -635,38 +628,31 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
 
   // Slots (one block update each, its own scheduling region):
-  //   First half (32 slots): B fragment reads in slots 0, 2, 4, 6; stage
-  //     writes every third slot from 1; the first four B loads every sixth
-  //     from 2, each behind the write that frees its registers.
-  //   Second half (32 slots): B fragment reads in slots 0, 2, 4, 6; A DMAs in
-  //     the odd slots below 16; the last four B loads every fourth slot from
-  //     17, after every DMA of their step (so the in-order waits for them,
-  //     which the stage writes take before the barrier that publishes the
-  //     step, cover the DMAs); A fragment i after slot 4i + 3.
+  //   First half (32 slots): B fragment reads in slots 0, 2, 4, 6.
+  //   Second half (32 slots): B fragment reads in slots 0, 2, 4, 6; B DMAs in
+  //     the odd slots below 16, A DMAs in the odd slots from 17; A fragment i
+  //     after slot 4i + 3.
   int slot = 0;  // A slot of the current step: kt % 3
-  auto step = [&](int kt, int s, i32x4 (&vnext)[NB]) __attribute__((always_inline)) {
+  auto step = [&](int kt, int s) __attribute__((always_inline)) {
     const int next_slot = slot == 2 ? 0 : slot + 1;
     static_for<0, 32>([&](auto q_c) __attribute__((always_inline)) {
       constexpr int q = decltype(q_c)::value, i = q / 4, j = 4 + q % 4;
       constexpr int rd = q < 8 && q % 2 == 0 ? q / 2 : -1;
       if constexpr (rd >= 0) fb[rd] = frag_b(s, rd);
-      constexpr int wr = q < 24 && q % 3 == 1 ? q / 3 : -1;
-      if constexpr (wr >= 0) store(vnext, s ^ 1, wr);
-      constexpr int ld = q < 24 && q % 6 == 2 ? q / 6 : -1;
-      if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
       mma(fa[i], fb[j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     });
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(8));
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, 32>([&](auto q_c) __attribute__((always_inline)) {
       constexpr int q = decltype(q_c)::value, i = q / 4, j = q % 4;
       constexpr int rd = q < 8 && q % 2 == 0 ? 4 + q / 2 : -1;
       if constexpr (rd >= 0) fb[rd] = frag_b(s ^ 1, rd);
-      constexpr int dm = q < 16 && q % 2 == 1 ? q / 2 : -1;
-      if constexpr (dm >= 0) dma_a(slot, min(kt + 3, last), dm);
-      constexpr int ld = q >= 17 && (q - 17) % 4 == 0 ? 4 + (q - 17) / 4 : -1;
-      if constexpr (ld >= 0) load(vnext, min(kt + 3, last), ld);
+      constexpr int db = q < 16 && q % 2 == 1 ? q / 2 : -1;
+      if constexpr (db >= 0) dma(rb, 3 + s, min(kt + 2, last), db);
+      constexpr int da = q >= 16 && q % 2 == 1 ? (q - 16) / 2 : -1;
+      if constexpr (da >= 0) dma(ra, slot, min(kt + 3, last), da);
       mma(fa[i], fb[j], acc[i][j]);
       if constexpr (j == 3) fa[i] = frag_a(next_slot, i);
       __builtin_amdgcn_sched_barrier(0);
@@ -674,8 +660,8 @@ __global__ void __launch_bounds__(256)
     slot = next_slot;
   };
   for (int kt = 0; kt < k_steps; kt += 2) {
-    step(kt, 0, v1);
-    step(kt + 1, 1, v0);
+    step(kt, 0);
+    step(kt + 1, 1);
   }
 #pragma unroll
   for (int i = 0; i < TILES; ++i)
