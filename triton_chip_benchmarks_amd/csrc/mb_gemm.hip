@@ -683,8 +683,8 @@ __global__ void __launch_bounds__(256)
 
 // ---- 256x128 kernel, A by LDS DMA (FP64 on 16x16x4) -------------------------
 
-// The DMA kernel's A ring, B stages, swizzle, pipeline and rolled fragments
-// for FP64 on a 256x128 tile: 256 accumulator registers hold 128x64 fp64
+// The 256x256 DMA kernel's A ring, swizzle, pipeline and rolled fragments,
+// with B through registers into two LDS stages, for FP64 on a 256x128 tile: 256 accumulator registers hold 128x64 fp64
 // outputs per wave (8x4 blocks of 16x16, four v_mfma_f64_16x16x4_f64 per
 // block per 128-byte step of 16 doubles). M a multiple of 256, N of 128, K an
 // even number of at least 4 steps.
@@ -878,7 +878,7 @@ void launch_gemm(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
       a, b, sa, sb, static_cast<typename Op::Out*>(c), m, n, k, group_m);
 }
 
-// The fast-path kernel of an instruction: the A-by-DMA kernel for the unscaled
+// The fast-path kernel of an instruction: the all-DMA kernel for the unscaled
 // ones (256x256; its 256x128 FP64 form), the register-staged kernel (with its
 // scale ring) for MXFP4.
 template <class Op>
