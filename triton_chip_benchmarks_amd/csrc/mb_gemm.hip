@@ -502,20 +502,24 @@ __global__ void __launch_bounds__(256)
 // one wait and barrier that split them in halves:
 //   first half:  blocks (i, 4 + j), i = 0..7, j = 0..3, row by row; reads of
 //                B fragments 0..3 of this step (their previous contents were
-//                last used at the end of the previous step), and no other
-//                memory traffic;
+//                last used at the end of the previous step); A of step kt+2
+//                DMAed into slot (kt+2) % 3, whose last reads (step kt-1's)
+//                ended before the previous barrier;
 //   wait         vmcnt(8): the wave's DMAs in flight are then at most the
 //                last eight it issued, step kt+2's A, so step kt+1's A (issued
-//                two steps back) and B (one step back) are in LDS;
+//                one half step back) and B (one step back) are in LDS;
 //   barrier      (publishes step kt+1 from every wave, and ends every read of
-//                A slot kt % 3 and of B slot s);
+//                B slot s);
 //   second half: blocks (i, j), i = 0..7, j = 0..3; at its start the reads
 //                of B fragments 4..7 of step kt+1, then A fragment i of step
 //                kt+1 right after block (i, 3), its last use; B of step kt+2
-//                DMAed into slot s, then A of step kt+3 into slot kt % 3.
-// The next step's first use of each fragment is at least 28 block updates
-// after its read. The compiler does not count the DMAs (they are inline
-// assembly), so the one explicit wait is what orders them before their reads.
+//                DMAed into slot s.
+// Each half issues its eight DMAs one every fourth block update: spread over
+// the whole step, they stall the load path less than in bursts (BF16 runs
+// 6-7% faster than with all sixteen in the second half). The next step's
+// first use of each fragment is at least 28 block updates after its read.
+// The compiler does not count the DMAs (they are inline assembly), so the one
+// explicit wait is what orders them before their reads.
 //
 // The MFMAs are issued in their in-place form (Op::mma_tied): the compiler
 // does not tie the 16-byte 16x16 instructions' accumulator input to their
@@ -603,10 +607,10 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < TILES; ++j) acc[i][j] = typename Op::Acc{};
 
-  // Prologue: A of steps 0..2 into A slots 0..2 and B of steps 0 and 1 into B
-  // slots 0 and 1, all of it in LDS before the barrier.
+  // Prologue: A and B of steps 0 and 1 into A slots 0, 1 and B slots 0, 1,
+  // all of it in LDS before the barrier.
 #pragma unroll
-  for (int p = 0; p < 3; ++p)
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
     for (int i = 0; i < 8; ++i) dma(ra, p, min(p, last), i);
 #pragma unroll
@@ -628,17 +632,19 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < TILES; ++j) acc_hazard_fence(acc[i][j]);
 
   // Slots (one block update each, its own scheduling region):
-  //   First half (32 slots): B fragment reads in slots 0, 2, 4, 6.
-  //   Second half (32 slots): B fragment reads in slots 0, 2, 4, 6; B DMAs in
-  //     the odd slots below 16, A DMAs in the odd slots from 17; A fragment i
-  //     after slot 4i + 3.
+  //   First half (32 slots): B fragment reads in slots 0, 2, 4, 6; A DMA i
+  //     in slot 4i + 1.
+  //   Second half (32 slots): B fragment reads in slots 0, 2, 4, 6; B DMA i in
+  //     slot 4i + 1; A fragment i after slot 4i + 3.
   int slot = 0;  // A slot of the current step: kt % 3
   auto step = [&](int kt, int s) __attribute__((always_inline)) {
-    const int next_slot = slot == 2 ? 0 : slot + 1;
+    const int next_slot = slot == 2 ? 0 : slot + 1, prev_slot = slot == 0 ? 2 : slot - 1;
     static_for<0, 32>([&](auto q_c) __attribute__((always_inline)) {
       constexpr int q = decltype(q_c)::value, i = q / 4, j = 4 + q % 4;
       constexpr int rd = q < 8 && q % 2 == 0 ? q / 2 : -1;
       if constexpr (rd >= 0) fb[rd] = frag_b(s, rd);
+      constexpr int da = q % 4 == 1 ? q / 4 : -1;
+      if constexpr (da >= 0) dma(ra, prev_slot, min(kt + 2, last), da);
       mma(fa[i], fb[j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -649,10 +655,8 @@ __global__ void __launch_bounds__(256)
       constexpr int q = decltype(q_c)::value, i = q / 4, j = q % 4;
       constexpr int rd = q < 8 && q % 2 == 0 ? 4 + q / 2 : -1;
       if constexpr (rd >= 0) fb[rd] = frag_b(s ^ 1, rd);
-      constexpr int db = q < 16 && q % 2 == 1 ? q / 2 : -1;
+      constexpr int db = q % 4 == 1 ? q / 4 : -1;
       if constexpr (db >= 0) dma(rb, 3 + s, min(kt + 2, last), db);
-      constexpr int da = q >= 16 && q % 2 == 1 ? (q - 16) / 2 : -1;
-      if constexpr (da >= 0) dma(ra, slot, min(kt + 3, last), da);
       mma(fa[i], fb[j], acc[i][j]);
       if constexpr (j == 3) fa[i] = frag_a(next_slot, i);
       __builtin_amdgcn_sched_barrier(0);
