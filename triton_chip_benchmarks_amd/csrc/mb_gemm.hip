@@ -507,7 +507,8 @@ __global__ void __launch_bounds__(256)
 //                ended before the previous barrier;
 //   wait         vmcnt(8): the wave's DMAs in flight are then at most the
 //                last eight it issued, step kt+2's A, so step kt+1's A (issued
-//                one half step back) and B (one step back) are in LDS;
+//                in step kt-1's first half) and B (in its second half) are in
+//                LDS;
 //   barrier      (publishes step kt+1 from every wave, and ends every read of
 //                B slot s);
 //   second half: blocks (i, j), i = 0..7, j = 0..3; at its start the reads
