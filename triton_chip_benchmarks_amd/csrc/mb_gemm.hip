@@ -494,7 +494,9 @@ __global__ void __launch_bounds__(256)
 // instructions, chunks 0..3 and then 4..7, so each block accumulates K in
 // chunk order. FP8 (16x16x128) takes it in one: the instruction's K order is
 // then a permutation of the step's, the same for A and B. Chunks 2g and 2g+1
-// would keep FP8's K order but measured LDS bank conflicts and 1% less. One
+// would keep FP8's K order but measured LDS bank conflicts and 1% less. FP32
+// (16x16x4) takes it in eight, instruction p taking float p of every lane's
+// 32 bytes (again the same K permutation for A and B). One
 // set of 8 A and 8 B fragments (128 VGPRs) is all the wave holds: every
 // fragment register is refilled in place after its last use.
 //
