@@ -7,8 +7,9 @@ in HBM. Each row is one configuration of the benchmark specification:
 
   hbm_copy        configs[0]  mb_copy of 2^28 fp32 (1 GiB, uniform[-1,1) from
                               seed 0) into a second buffer; bit-exact
-  peak_bf16       configs[2]  resident-operand variant: a 128x128x64 BF16 tile,
-                              2 chains, looped 1024 times per workgroup, 4 per CU
+  peak_bf16       configs[2]  resident-operand variant: a 256x256x64 BF16 LDS
+                              tile looped 1024 times per workgroup, 1 chain,
+                              2 workgroups per CU, in-place 16x16 MFMAs
   gemm_bf16       configs[2]  BF16 GEMM 8192^3, A, B ~ N(0,1), B column-major
   gemm_fp16       configs[2]  FP16 GEMM 8192^3, same operands
   gemm_fp8        configs[3]  FP8 E4M3 GEMM 8192^3 over {+-0.5, +-1, +-2}; exact
@@ -16,6 +17,9 @@ in HBM. Each row is one configuration of the benchmark specification:
   gemm_fp64       configs[3]  FP64 GEMM 4096^3, N(0,1)
   gemm_mxfp4      configs[4]  MXFP4 GEMM 16384^3, all 16 E2M1 codes, E8M0
                               scale 127 per 32 K elements; exact
+  peak_bf16_128x128_c2        the 128x128x64 BF16 tile with 2 chains, 4 per CU
+                              (a smaller tile than the specification's; not
+                              in the headline mean)
   peak_fp8        17-row table: FP8 resident tile 128x128x128, 2 chains,
                               the reference's one-hot operands
   peak_fp8_dense  the same kernel on the dense {+-0.5, +-1, +-2} set
@@ -51,6 +55,17 @@ torch.cuda.synchronize(), with HIP events on the launch stream between
 sub-batches of about --sub-batch-ms. ms_per_launch is the whole timed region
 over --steps; min and median are over the sub-batch averages.
 
+Between a row's warmup and its timed launches, a one-wave clock witness on a
+second stream measures the engine clock its kernel sustains (ClockWitness);
+the row reports it with frac_at_clock = rate / (peak * clock / 2400 MHz).
+
+Output: ONE JSON line on stdout, kept under 8 KiB (the contract fields, the
+roofline of the dominant headline kernel, a compact cpu_baseline and, per row,
+name, kernel, value, unit, fraction, ms per launch, clock and frac_at_clock);
+the full per-row records (configuration, validation, min/median, warmup,
+traffic, per-row CPU figures, clock measurement) go to the --detail file,
+whose path the line names.
+
 cpu_baseline times the reference's own host arithmetic for each row on this
 machine's cores (torch.Tensor.copy_ of 1 GiB; torch.matmul in fp32, fp64
 for FP64, on sampled rows of the same GEMM shape or a batch of the same
@@ -85,6 +100,12 @@ VECTOR_ITERATIONS = 4096
 VECTOR_SEED = 0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_per_launch.txt"
 CPU_ROW_BUDGET_S = 2.0
+# The stdout line's bound: a driver that keeps the tail of stdout must see all of it.
+MAX_LINE_BYTES = 8192
+# Clock witness of a row: real-time interval it measures, inside launches of the row's kernel lasting
+# CLOCK_LOAD_MS, between the warmup and the timed launches.
+CLOCK_WITNESS_MS = 100.0
+CLOCK_LOAD_MS = 150.0
 
 
 def parse_args(argv=None):
@@ -99,6 +120,10 @@ def parse_args(argv=None):
                         help="device time between two events inside the timed launches (default: 2)")
     parser.add_argument("--no-cpu-baseline", action="store_true", help="skip the host CPU leg")
     parser.add_argument("--rows", nargs="+", help="subset of rows to run (default: all)")
+    parser.add_argument("--detail", default=str(ROOT / "results" / "bench_detail.json"),
+                        help="file for the full per-row records (default: results/bench_detail.json)")
+    parser.add_argument("--no-clock", action="store_true",
+                        help="do not measure the engine clock each row's kernel runs at")
     return parser.parse_args(argv)
 
 
@@ -337,13 +362,14 @@ def _row_specs():
 
     return [
         ("hbm_copy", CopyWorkload),
-        peak("peak_bf16", "bf16", (128, 128, 64), 2, 4),
+        peak("peak_bf16", "bf16", (256, 256, 64), 1, 2),
         gemm("gemm_bf16", "bf16", 8192),
         gemm("gemm_fp16", "fp16", 8192),
         gemm("gemm_fp8", "fp8", 8192),
         gemm("gemm_int8", "int8", 8192),
         gemm("gemm_fp64", "fp64", 4096),
         gemm("gemm_mxfp4", "fp4", 16384),
+        peak("peak_bf16_128x128_c2", "bf16", (128, 128, 64), 2, 4),
         peak("peak_fp8", "fp8", (128, 128, 128), 2, 4),
         peak("peak_fp8_dense", "fp8", (128, 128, 128), 2, 4, "dense"),
         peak("peak_mxfp4", "fp4", (128, 128, 256), 2, 4),
@@ -369,6 +395,37 @@ class _Events:
                 raise RuntimeError(f"invalid device event time {ms!r} ms")
             out.append((n1 - n0, ms))
         return out
+
+
+class ClockWitness:
+    """The engine clock a row's kernel sustains (mb_clock_witness), measured on the device.
+
+    One sleeping wave on a second stream counts shader clock cycles against the constant-rate real-time counter
+    for CLOCK_WITNESS_MS while the row's kernel runs back to back for CLOCK_LOAD_MS on the launch stream, after
+    its warmup (the same steady load the timed launches see) and outside the timed region. The clock is that of
+    the witness's CU; rate / (peak * clock / 2400 MHz) then separates a low-clock box from a slow kernel.
+    """
+
+    def __init__(self, torch, native):
+        self.torch, self.native = torch, native
+        self.side = torch.cuda.Stream()
+        self.out = torch.zeros(4, dtype=torch.int64, device="cuda")
+        self.wall_khz = native.wall_clock_khz()
+
+    def measure(self, stream, workload, estimate_ms: float) -> dict:
+        launches = max(2, math.ceil(CLOCK_LOAD_MS / max(estimate_ms, 1e-3)))
+        self.out.zero_()
+        self.torch.cuda.synchronize()
+        self.native.clock_witness(self.out, int(CLOCK_WITNESS_MS * 1000), self.side)
+        for _ in range(launches):
+            workload.launch()
+        self.torch.cuda.synchronize()
+        cycles, ticks, polls, _start = (int(v) for v in self.out.tolist())
+        complete = ticks >= CLOCK_WITNESS_MS * self.wall_khz * 0.999
+        return {"clock_mhz": cycles / ticks * self.wall_khz / 1000 if ticks and complete else None,
+                "witness_ms": ticks / self.wall_khz, "polls": polls, "load_launches": launches,
+                "method": "mb_clock_witness: s_memtime cycles / s_memrealtime ticks of one wave beside the "
+                          "kernel's launches"}
 
 
 def warm(torch, stream, workload, min_launches, min_ms):
@@ -445,10 +502,12 @@ def main(argv=None):
         validation = workload.check()
         workloads.append((workload, validation))
 
+    witness = None if args.no_clock else ClockWitness(torch, _native)
     for workload, validation in workloads:
         print(f"[bench] {workload.name}: warmup and {args.steps} timed launches", file=sys.stderr, flush=True)
         warm_launches, warm_ms, estimate = warm(torch, stream, workload, args.warmup, args.warmup_ms)
         per_batch = max(1, min(args.steps, round(args.sub_batch_ms / estimate)))
+        clock = witness.measure(stream, workload, estimate) if witness is not None else None
         workload.poison()  # the timed launches must rewrite the whole output
         samples = time_launches(torch, stream, workload, args.steps, per_batch)
         workload.check()  # raises if the timed launches' output is wrong
@@ -469,24 +528,17 @@ def main(argv=None):
             "warmup_launches": warm_launches, "warmup_device_ms": warm_ms,
             "algorithmic_work_per_launch": workload.work, "work_unit": "bytes" if workload.bound == "hbm" else "flop",
             "traffic_bytes_per_launch": traffic.get(workload.kernel), "dtype": workload.label,
-            "config": workload.config, "validation": validation})
+            "clock": clock, "config": workload.config, "validation": validation})
+        if clock and clock["clock_mhz"] and workload.bound != "hbm":
+            # The same work per clock at the clock this kernel ran at: separates a low-clock box from a slow kernel.
+            rows[-1]["frac_at_clock"] = achieved / (peak * clock["clock_mhz"] / roofline.PEAK_CLOCK_MHZ)
         if workload.row in roofline.ISSUED_CEILINGS:  # the instruction this build issues is slower than the datasheet's
             ceiling, ceiling_basis = roofline.ISSUED_CEILINGS[workload.row]
             rows[-1].update(issued_instruction_ceiling=ceiling, issued_instruction_basis=ceiling_basis,
                             frac_of_issued_ceiling=achieved / ceiling)
 
-    headline = [r for r in rows if r["in_headline"]] or rows
-    value = 100.0 * sum(r["frac"] for r in headline) / len(headline)
-    dominant = max(headline, key=lambda r: r["ms_per_launch"])
-    roofline_block = {"bound": dominant["bound"], "kernel": dominant["kernel"], "row": dominant["name"],
-                      "achieved": dominant["value"], "peak": dominant["peak"], "unit": dominant["unit"],
-                      "frac": dominant["frac"], "traffic": dominant["traffic_bytes_per_launch"],
-                      "algorithmic_work_per_launch": dominant["algorithmic_work_per_launch"],
-                      "ms_per_launch": dominant["ms_per_launch"]}
-    cpu = None
+    cpu_rows = None
     if not args.no_cpu_baseline:
-        from triton_chip_benchmarks_amd.cpu_baseline import host_description
-
         cpu_rows = []
         for workload, _ in workloads:
             print(f"[bench] {workload.name}: host CPU baseline", file=sys.stderr, flush=True)
@@ -495,13 +547,33 @@ def main(argv=None):
             cpu_rows.append({"name": workload.name, "value": result["value"], "unit": result["unit"],
                              "cores": result["cores"], "method": result["method"], "sample": result["sample"],
                              "frac_of_mi355x_peak": result["value"] / peak})
+    from triton_chip_benchmarks_amd.cpu_baseline import host_description
+
+    document = full_document(args, info, rows, cpu_rows, host_description() if cpu_rows else None)
+    detail = Path(args.detail)
+    detail.parent.mkdir(parents=True, exist_ok=True)
+    detail.write_text(json.dumps(document, indent=1) + "\n")
+    print(json.dumps(headline_line(document, str(detail))))
+    return 0
+
+
+def full_document(args, info, rows, cpu_rows, host) -> dict:
+    """Every figure of the run: the contract fields plus the full per-row records."""
+    headline = [r for r in rows if r["in_headline"]] or rows
+    value = 100.0 * sum(r["frac"] for r in headline) / len(headline)
+    dominant = max(headline, key=lambda r: r["ms_per_launch"])
+    roofline_block = {"bound": dominant["bound"], "kernel": dominant["kernel"], "row": dominant["name"],
+                      "achieved": dominant["value"], "peak": dominant["peak"], "unit": dominant["unit"],
+                      "frac": dominant["frac"], "traffic": dominant["traffic_bytes_per_launch"],
+                      "algorithmic_work_per_launch": dominant["algorithmic_work_per_launch"],
+                      "work_unit": dominant["work_unit"], "ms_per_launch": dominant["ms_per_launch"]}
+    cpu = None
+    if cpu_rows:
         in_mean = [r for r in cpu_rows if r["name"] in HEADLINE] or cpu_rows
         cpu = {"value": 100.0 * sum(r["frac_of_mi355x_peak"] for r in in_mean) / len(in_mean),
                "unit": "% of MI355X peak (mean over the headline rows)", "cores": max(r["cores"] for r in cpu_rows),
-               "kind": "port",
-               "sample": "; ".join(f"{r['name']}: {r['method']}, {r['sample']}" for r in cpu_rows),
-               "host": host_description(), "rows": cpu_rows}
-    line = {
+               "kind": "port", "host": host, "rows": cpu_rows}
+    return {
         "metric": METRIC, "value": value, "unit": "% of MI355X peak (mean over the headline rows)",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": sum(r["ms_per_launch"] for r in rows), "higher_is_better": True, "scaling": "weak",
@@ -519,8 +591,51 @@ def main(argv=None):
                              "`steps` launches with HIP events on the launch stream between sub-batches"},
         "roofline": roofline_block, "cpu_baseline": cpu, "rows": rows,
     }
-    print(json.dumps(line))
-    return 0
+
+
+def _round(value, digits=5):
+    """`value` to `digits` significant digits (None and non-floats unchanged)."""
+    if not isinstance(value, float) or not math.isfinite(value) or value == 0.0:
+        return value
+    return round(value, digits - 1 - int(math.floor(math.log10(abs(value)))))
+
+
+def headline_line(document: dict, detail_path: str) -> dict:
+    """The one stdout line: contract fields, roofline, a compact cpu_baseline and short rows (< MAX_LINE_BYTES)."""
+    cpu = document["cpu_baseline"]
+    compact_cpu = None
+    if cpu:
+        host = cpu.get("host") or {}
+        sample = "; ".join(f"{r['name']} {_round(r['value'], 3)} {r['unit']}" for r in cpu["rows"]
+                           if r["name"] in HEADLINE)
+        compact_cpu = {"value": _round(cpu["value"]), "unit": cpu["unit"], "cores": cpu["cores"], "kind": cpu["kind"],
+                       "sample": ("torch CPU path per headline row, bounded sample each: " + sample)[:200],
+                       "host": f"{host.get('cpu_model')}, {host.get('usable_cpus')} usable CPUs"[:120]}
+    rows = []
+    for r in document["rows"]:
+        row = {"name": r["name"], "kernel": r["kernel"], "value": _round(r["value"]), "unit": r["unit"],
+               "frac": _round(r["frac"], 4), "ms_per_launch": _round(r["ms_per_launch"], 4),
+               "in_headline": r["in_headline"]}
+        clock = r.get("clock") or {}
+        if clock.get("clock_mhz"):
+            row["clock_mhz"] = round(clock["clock_mhz"])
+        if "frac_at_clock" in r:
+            row["frac_at_clock"] = _round(r["frac_at_clock"], 4)
+        rows.append(row)
+    roofline_block = {key: _round(value) for key, value in document["roofline"].items()}
+    line = {key: document[key] for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                                           "higher_is_better", "scaling", "vs_baseline", "dtype", "data")}
+    line["value"], line["ms_per_step"] = _round(line["value"]), _round(line["ms_per_step"])
+    config = document["config"]
+    line["config"] = {"workload": config["workload"], "device": config["device"], "arch": config["arch"],
+                      "compute_units": config["compute_units"]}
+    line.update(roofline=roofline_block, cpu_baseline=compact_cpu, rows=rows, detail=detail_path)
+    if len(json.dumps(line).encode()) > MAX_LINE_BYTES:  # never let the line outgrow what a reader keeps
+        for row in line["rows"]:
+            row.pop("kernel", None)
+    if len(json.dumps(line).encode()) > MAX_LINE_BYTES:
+        line["rows"] = [{"name": r["name"], "frac": r["frac"]} for r in line["rows"]]
+    return line
 
 
 if __name__ == "__main__":

@@ -78,6 +78,23 @@ const char* mb_kernel_name(int index);
  * metadata.shared (bench_tensor.py:1134-1136, bench_vector.py:625-627). */
 int mb_kernel_attributes_query(const char* name, mb_kernel_attributes* out);
 
+/* ---- engine clock -------------------------------------------------------- */
+
+/* Rate of the device's constant real-time counter (hipDeviceAttributeWallClockRate) of the current device, in kHz. */
+int mb_wall_clock_khz(int* khz);
+
+/* Launches one wave on `stream` that measures the engine clock of its CU over
+ * `microseconds` (1..10^7) of real time while other work runs: out[0] =
+ * shader clock cycles (s_memtime), out[1] = real-time counter ticks
+ * (s_memrealtime) over the same interval, out[2] = polls made, out[3] = the
+ * real-time counter at the start. clock in kHz = out[0] / out[1] *
+ * mb_wall_clock_khz. `out` holds 4 uint64 in device memory. The wave sleeps
+ * between polls; the loop also ends after a bounded number of polls, so
+ * out[1] below the requested interval means it ended early.
+ * No counterpart in the reference (its rows report no clock); it serves the
+ * headline benchmark, which records the clock each row's kernel ran at. */
+int mb_clock_witness(uint64_t* out, uint64_t out_bytes, uint32_t microseconds, void* stream);
+
 /* ---- memory: copy and read ---------------------------------------------- */
 
 /* Flags for mb_copy. */

@@ -156,10 +156,12 @@ def gemm_reference(a: np.ndarray, b: np.ndarray) -> np.ndarray:
 
 
 # Elementwise GEMM tolerance, rtol = atol (bench_tensor.py:289-299 uses
-# torch.testing.assert_close with rtol = atol). BF16/FP16 and FP64 take the
-# benchmark configuration's 1e-2 and 1e-12; FP32 keeps the reference's 2e-3;
+# torch.testing.assert_close with rtol = atol). BF16, FP16 and FP32 take the
+# reference's 2e-3 (bench_tensor.py:292-293; published as rtol = atol = 0.002
+# on its FP16 GEMM rows), tighter than the benchmark configuration's 1e-2;
+# FP64 takes the configuration's 1e-12, tighter than the reference's 1e-10;
 # the FP8, INT8 and MXFP4 operand sets are exact in the accumulator, so 0.
-GEMM_TOLERANCE = {"bf16": 1e-2, "fp16": 1e-2, "fp32": 2e-3, "fp64": 1e-12, "fp8": 0.0, "int8": 0.0, "fp4": 0.0}
+GEMM_TOLERANCE = {"bf16": 2e-3, "fp16": 2e-3, "fp32": 2e-3, "fp64": 1e-12, "fp8": 0.0, "int8": 0.0, "fp4": 0.0}
 
 
 def gemm_close(actual: np.ndarray, reference: np.ndarray, rtol: float, atol: float) -> np.ndarray:

@@ -66,6 +66,20 @@ def main(reference):
     out["memory_capacity"] = {"source": "results/bw1100_metrics_runs/memory_capacity.json device",
                               "total_memory_bytes": capacity["device"]["total_memory_bytes"],
                               "memory_capacity_gib": capacity["device"]["memory_capacity_gib"]}
+    # The reference's GEMM mode on its own operand recipe (bench_tensor.py:249-299, 1509-1595): the
+    # best-rate row per size of its FP16 run, with the tolerance it was checked at.
+    gemm = json.loads((root / "results/h20_tensor.json").read_text())
+    best = {}
+    for row in gemm["results"]:
+        if row.get("status") == "ok" and (row["m"] not in best or row["tflops"] > best[row["m"]]["tflops"]):
+            best[row["m"]] = row
+    out["gemm_fp16_h20"] = {
+        "source": "results/h20_tensor.json results (best tflops per size)", "dtype": gemm["arguments"]["dtype"],
+        "sizes": gemm["arguments"]["sizes"], "device": gemm["device"].get("device_name"),
+        "rows": [{"m": r["m"], "n": r["n"], "k": r["k"], "flops": r["flops"], "tflops": r["tflops"],
+                  "rtol": r["correctness"]["rtol"], "atol": r["correctness"]["atol"],
+                  "max_abs_error": r["correctness"]["max_abs_error"], "config": r["config"]}
+                 for r in (best[m] for m in sorted(best))]}
     # Known answers stated in the reference's tests.
     out["e2m1_packing"] = {"source": "tests/test_tensor_formats.py:55-64",
                            "codes": [[1, 2, 9, 10]], "packed": [[2 << 4 | 1, 10 << 4 | 9]],

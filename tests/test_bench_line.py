@@ -1,0 +1,101 @@
+"""CPU tests of bench.py's stdout line: the contract fields, and a length bound that holds for a full row set.
+
+A reader that keeps only the tail of stdout (about 10 KB) must still see the whole line, so the line is built from
+compact rows and the full per-row records go to the detail file. These tests build the line from fake rows as long
+as the real ones (every row of the run, long validation, config and CPU sample strings) and check the bound.
+"""
+
+import argparse
+import json
+import math
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+CONTRACT = {"metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+            "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"}
+
+
+def _fake_rows():
+    names = [name for name, _ in bench._row_specs()]
+    rows = []
+    for index, name in enumerate(names):
+        unit = "GB/s" if name == "hbm_copy" else "TOP/s" if "int8" in name else "TFLOP/s"
+        peak = 8000.0 if unit == "GB/s" else 2516.5824
+        value = peak * (0.5 + index / 100.0) + 1.0 / 3.0
+        rows.append({
+            "name": name, "row": "tensor_bf16", "in_headline": name in bench.HEADLINE,
+            "kernel": f"tensor_peak_bf16_256x256x64_c1_mfma16_kn_{'x' * 20}", "value": value, "unit": unit,
+            "peak": peak, "frac": value / peak, "peak_basis": "datasheet " * 10, "bound": "mfma",
+            "ms_per_launch": 1.0 + index / 7.0, "min_ms_per_launch": 1.0, "median_ms_per_launch": 1.0,
+            "value_at_min": value, "value_at_median": value, "sub_batches": 10, "launches_per_sub_batch": 2,
+            "warmup_launches": 200, "warmup_device_ms": 250.0, "algorithmic_work_per_launch": 4.398046511104e12,
+            "work_unit": "flop", "traffic_bytes_per_launch": 1.23456789e9, "dtype": "bf16",
+            "clock": {"clock_mhz": 2011.123, "witness_ms": 100.0, "polls": 753762, "load_launches": 200,
+                      "method": "mb_clock_witness: s_memtime cycles / s_memrealtime ticks of one wave beside the "
+                                "kernel's launches"},
+            "frac_at_clock": 0.97, "config": {"text": "c" * 400}, "validation": "v" * 1500})
+    return rows
+
+
+def _fake_document():
+    args = argparse.Namespace(steps=20, warmup=5, warmup_ms=250.0, sub_batch_ms=2.0)
+    info = {"name": "AMD Instinct MI355X", "arch": "gfx950:sramecc+:xnack-", "compute_units": 256}
+    rows = _fake_rows()
+    cpu_rows = [{"name": r["name"], "value": 1.2345678, "unit": r["unit"], "cores": 16, "method": "m" * 300,
+                 "sample": "s" * 2000, "frac_of_mi355x_peak": 1e-3} for r in rows]
+    host = {"cpu_model": "AMD EPYC 9575F 64-Core Processor", "usable_cpus": 16}
+    return bench.full_document(args, info, rows, cpu_rows, host)
+
+
+def test_line_of_a_full_row_set_stays_under_the_bound():
+    line = bench.headline_line(_fake_document(), "results/bench_detail.json")
+    encoded = json.dumps(line).encode()
+    assert len(encoded) <= bench.MAX_LINE_BYTES == 8192, len(encoded)
+    # Room to spare: the real rows are no longer than the fake ones.
+    assert len(encoded) <= 6500, len(encoded)
+
+
+def test_line_keeps_the_contract_fields_and_every_row():
+    document = _fake_document()
+    line = bench.headline_line(document, "results/bench_detail.json")
+    assert CONTRACT <= set(line)
+    assert line["n_gpus"] == 1 and line["steps"] == 20 and line["warmup"] == 5
+    assert line["detail"] == "results/bench_detail.json"
+    assert "workload" in line["config"] and "model" not in line["config"]
+    assert [r["name"] for r in line["rows"]] == [r["name"] for r in document["rows"]]
+    for row in line["rows"]:
+        assert {"name", "kernel", "value", "unit", "frac", "ms_per_launch", "in_headline", "clock_mhz",
+                "frac_at_clock"} <= set(row)
+    headline = [r for r in document["rows"] if r["in_headline"]]
+    assert line["value"] == pytest.approx(100 * sum(r["frac"] for r in headline) / len(headline), rel=1e-4)
+    roofline = line["roofline"]
+    assert {"bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "algorithmic_work_per_launch",
+            "ms_per_launch"} <= set(roofline)
+    assert roofline["frac"] == pytest.approx(roofline["achieved"] / roofline["peak"], rel=1e-4)
+    dominant = max(headline, key=lambda r: r["ms_per_launch"])
+    assert roofline["row"] == dominant["name"]
+    cpu = line["cpu_baseline"]
+    assert {"value", "unit", "cores", "kind", "sample"} <= set(cpu)
+    assert len(cpu["sample"]) <= 200 and cpu["kind"] == "port" and cpu["cores"] == 16
+
+
+def test_line_falls_back_to_bare_rows_before_it_outgrows_the_bound(monkeypatch):
+    monkeypatch.setattr(bench, "MAX_LINE_BYTES", 3000)
+    line = bench.headline_line(_fake_document(), "results/bench_detail.json")
+    assert len(json.dumps(line).encode()) <= 3000
+    assert all(set(row) == {"name", "frac"} for row in line["rows"])
+    assert CONTRACT <= set(line)
+
+
+def test_rounding_keeps_significant_digits():
+    assert bench._round(2283.987654) == 2284.0
+    assert bench._round(0.000123456789) == pytest.approx(0.00012346)
+    assert bench._round(None) is None and bench._round(7) == 7
+    assert math.isnan(bench._round(float("nan")))

@@ -254,3 +254,70 @@ def test_mxfp4_gemm_applies_each_rows_group_scale(gpu):
             expected = ot.gemm_reference(a_values, b_values.T)
             got = c.cpu().numpy().astype(np.float64)
             assert np.array_equal(got, expected), f"max error {np.abs(got - expected).max()}"
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32", "fp64", "int8"])
+def test_reference_recipe_ragged_shape_matches_oracle(gpu, dtype):
+    """The reference's own operands (bench_tensor.py:249-261: N(0,1) A, N(0,1)/sqrt(K) B drawn [K][N], INT8
+    {-1,0,1}) at a ragged shape on every tile, every entry against the float64 oracle at the reference's
+    tolerance (bench_tensor.py:289-299: 2e-3, 1e-10 FP64, exact INT8)."""
+    import torch
+
+    from triton_chip_benchmarks_amd import _native, gemm
+
+    m, n, k = 1000, 744, {"int8": 1008, "fp64": 1000, "fp32": 1000}.get(dtype, 1000)
+    for config in _configs(dtype):
+        print(f"gemm {dtype} reference recipe tile {config['tile_m']}x{config['tile_n']}x{config['tile_k']} "
+              f"shape {m}x{n}x{k}", flush=True)
+        a, b, c, _scales, a_values, b_values = gemm.gemm_inputs(dtype, m, n, k, "cuda", 9, inputs="reference")
+        c.fill_(-3)
+        _native.gemm(dtype, config, a, b, c, m, n, k)
+        torch.cuda.synchronize()
+        got = c.cpu().numpy().astype(np.float64)
+        expected = ot.gemm_reference(a_values.cpu().numpy(), b_values.cpu().numpy().T)
+        tolerance = gemm.REFERENCE_TOLERANCE[dtype]
+        if tolerance == 0.0:
+            assert np.array_equal(got, expected)
+        else:
+            assert np.all(ot.gemm_close(got, expected, tolerance, tolerance)), np.abs(got - expected).max()
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_reference_recipe_8192_diffs_against_the_published_row(gpu, dtype):
+    """8192^3 on the reference recipe, the size of its published FP16 row (results/h20_tensor.json,
+    max abs error 7.49e-5 at rtol = atol = 2e-3): sampled rows against the oracle, both checksums, and every
+    entry through the product's float64 device check at the reference's tolerance."""
+    import json
+    from pathlib import Path
+
+    import torch
+
+    from triton_chip_benchmarks_amd import _native, gemm
+
+    size = 8192
+    published = {row["m"]: row for row in
+                 json.loads((Path(__file__).parent / "golden" / "reference_published.json").read_text())
+                 ["gemm_fp16_h20"]["rows"]}[size]
+    config = max(_configs(dtype), key=lambda c: c["tile_m"] * c["tile_n"])
+    print(f"gemm {dtype} reference recipe {size}^3 tile {config['tile_m']}x{config['tile_n']}", flush=True)
+    a, b, c, _scales, a_values, b_values = gemm.gemm_inputs(dtype, size, size, size, "cuda", 0, inputs="reference")
+    c.fill_(float("nan"))
+    _native.gemm(dtype, config, a, b, c, size, size, size)
+    torch.cuda.synchronize()
+    result = gemm.validate(c, gemm.reference(a_values, b_values), dtype, tolerance=gemm.REFERENCE_TOLERANCE[dtype])
+    assert result["rtol"] == published["rtol"] and result["atol"] == published["atol"]
+    print(f"  max abs error {result['max_abs_error']:.3g} (published H20 FP16 row: {published['max_abs_error']:.3g})",
+          flush=True)
+    # |C| ~ N(0,1) entries from an fp32 accumulation of 8192 products: errors of order 1e-4, as published.
+    assert result["max_abs_error"] < 20 * published["max_abs_error"]
+    host_a, host_b = a_values.cpu().numpy(), b_values.cpu().numpy()
+    got = c.cpu().numpy().astype(np.float64)
+    rng = np.random.default_rng(8)
+    rows = rng.choice(size, 8, replace=False)
+    sampled = ot.gemm_reference(host_a[rows], host_b.T)
+    assert np.all(ot.gemm_close(got[rows], sampled, 2e-3, 2e-3))
+    b_kn = host_b.T
+    column_sums = ot.gemm_reference(host_a.sum(axis=0)[None, :], b_kn)[0]
+    row_sums = ot.gemm_reference(host_a, host_b.sum(axis=0)[:, None])[:, 0]
+    assert np.all(np.abs(got.sum(axis=0) - column_sums) <= ot.checksum_tolerance(host_a, b_kn, dtype, 0))
+    assert np.all(np.abs(got.sum(axis=1) - row_sums) <= ot.checksum_tolerance(host_a, b_kn, dtype, 1))

@@ -88,6 +88,37 @@ def test_peak_matches_oracle_every_tile(gpu, dtype, iterations):
             f"{dtype} {config}: max error {np.nanmax(error)}")
 
 
+@pytest.mark.parametrize("b_nk", [0, 1])
+def test_specification_resident_bf16_tile_at_1024_iterations(gpu, b_nk):
+    """The headline resident BF16 configuration: a 256x256x64 tile looped 1024 times per workgroup.
+
+    The 16x16 in-place kernel (bench.py's peak_bf16 row) on the reference's ternary/16 lattice
+    (bench_tensor.py:651-672), against oracle.tensor.peak_reference under the reference's tolerance
+    (bench_tensor.py:302-346), with 64 workgroups so that every wave position of the tile is covered many times.
+    """
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+
+    config = next(c for c in _native.peak_configs("bf16") if (c["tile_m"], c["tile_n"], c["tile_k"]) == (256, 256, 64)
+                  and c["mfma_m"] == 16 and c["chains"] == 1 and c["b_nk"] == b_nk)
+    assert _native.peak_kernel_name("bf16", config) == f"tensor_peak_bf16_256x256x64_c1_mfma16_{'nk' if b_nk else 'kn'}"
+    rng = np.random.default_rng(256 + b_nk)
+    blocks, iterations = 64, 1024
+    print(f"peak bf16 256x256x64 c1 mfma16 nk={b_nk} blocks={blocks} iterations={iterations}", flush=True)
+    a_values = ot.ternary_lattice(rng, (blocks, 256, 64))
+    b_values = ot.ternary_lattice(rng, (1, blocks, 64, 256))
+    a = _encode(torch, a_values, "bf16")
+    b = _encode(torch, np.swapaxes(b_values, -1, -2) if b_nk else b_values, "bf16")
+    c = torch.full((1, blocks, 256, 256), float("nan"), dtype=torch.float32, device="cuda")
+    _native.tensor_peak("bf16", config, a, b, c, blocks, iterations)
+    torch.cuda.synchronize()
+    reference = ot.peak_reference(a_values, b_values, iterations)
+    error = np.abs(c.cpu().numpy().astype(np.float64) - reference)
+    assert np.all(error <= ot.peak_tolerance("bf16", 64, iterations)), f"max error {np.nanmax(error)}"
+    assert np.count_nonzero(reference) > reference.size // 2  # the lattice is not a trivial product
+
+
 @pytest.mark.parametrize("iterations", [1, 5])
 def test_mxfp4_all_codes_and_scales_match_oracle(gpu, iterations):
     """All 16 E2M1 codes, packed two per byte; E8M0 scales 126..128 per 32-K group."""

@@ -240,6 +240,58 @@ def test_peak_reference_is_iterations_times_the_tile_product():
         ot.check_peak(wrong, reference, "bf16", 16, 5)
 
 
+def test_one_hot_rows_have_exactly_one_entry_and_make_every_dot_a_lattice_step():
+    """The reference's FP8 A (bench_tensor.py:651-658): each row one 1/16 at a K position, so against
+    B = +-1/16 every dot is exactly +-1/256. A hot entry on the wrong axis, two per row, or the wrong
+    value breaks one of these."""
+    rng = np.random.default_rng(12)
+    a = ot.one_hot_rows(rng, (3, 64, 32))
+    assert a.shape == (3, 64, 32)
+    assert np.array_equal(np.count_nonzero(a, axis=-1), np.ones((3, 64), dtype=np.int64))
+    assert set(np.unique(a)) == {0.0, 1 / 16}
+    # The hot positions cover the K axis (uniform over 32 positions: 192 rows miss one with odds ~ 1e-2).
+    assert len(np.unique(np.argmax(a, axis=-1))) >= 28
+    b = (2.0 * rng.integers(0, 2, (2, 3, 32, 16)) - 1.0) / 16
+    product = ot.peak_reference(a, b, 1)
+    assert set(np.unique(np.abs(product))) == {1 / 256}
+    # The product picks row k_hot of B: C[c, w, i, :] = B[c, w, k_hot(w, i), :] / 16.
+    hot = np.argmax(a, axis=-1)
+    for c in range(2):
+        for w in range(3):
+            assert np.array_equal(product[c, w], b[c, w, hot[w]] / 16)
+
+
+def test_product_fp8_peak_operands_are_one_hot_rows():
+    """bench_tensor.peak_inputs builds the reference's FP8 operands with torch: its A must satisfy the same
+    one-hot invariant as oracle.tensor.one_hot_rows, and its B be +-1/16, so the exact reference is +-1/256."""
+    torch = pytest.importorskip("torch")
+    from triton_chip_benchmarks_amd import bench_tensor
+
+    config = {"tile_m": 32, "tile_n": 16, "tile_k": 64, "chains": 2, "b_nk": 0}
+    a, _b, _c, b_logical = bench_tensor.peak_inputs(3, config, "fp8", "cpu", seed=4)
+    a_values, b_values = a.to(torch.float64).numpy(), b_logical.to(torch.float64).numpy()
+    assert np.array_equal(np.count_nonzero(a_values, axis=-1), np.ones((3, 32), dtype=np.int64))
+    assert set(np.unique(a_values)) == {0.0, 1 / 16}
+    assert set(np.unique(b_values)) == {-1 / 16, 1 / 16}
+    assert set(np.unique(np.abs(ot.peak_reference(a_values, b_values, 1)))) == {1 / 256}
+
+
+def test_gemm_tolerance_is_the_reference_published_one():
+    """BF16/FP16/FP32 GEMM verdicts use rtol = atol = 2e-3, the value the reference's FP16 GEMM rows were
+    checked at (bench_tensor.py:292-293; results/h20_tensor.json), and the product uses the same table."""
+    from triton_chip_benchmarks_amd import gemm
+
+    published = GOLDEN["gemm_fp16_h20"]
+    assert {(row["rtol"], row["atol"]) for row in published["rows"]} == {(0.002, 0.002)}
+    for dtype in ("bf16", "fp16", "fp32"):
+        assert ot.GEMM_TOLERANCE[dtype] == 0.002
+        assert gemm.TOLERANCE[dtype] == ot.GEMM_TOLERANCE[dtype]
+        assert gemm.REFERENCE_TOLERANCE[dtype] == 0.002
+    assert gemm.TOLERANCE == ot.GEMM_TOLERANCE
+    assert gemm.REFERENCE_SIZES == published["sizes"]
+    assert [row["flops"] for row in published["rows"]] == [2 * size**3 for size in published["sizes"]]
+
+
 # ---- memory oracle ----------------------------------------------------------------------------
 
 def test_bandwidth_traffic_matches_published_rows():

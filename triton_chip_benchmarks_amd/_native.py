@@ -93,6 +93,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mb_kernel_count": (_i32, []),
     "mb_kernel_name": (ctypes.c_char_p, [_i32]),
     "mb_kernel_attributes_query": (_i32, [ctypes.c_char_p, ctypes.POINTER(KernelAttributes)]),
+    "mb_wall_clock_khz": (_i32, [ctypes.POINTER(_i32)]),
+    "mb_clock_witness": (_i32, [_ptr, _u64, _u32, _ptr]),
     "mb_copy": (_i32, [_ptr, _ptr, _u64, _u32, _u32, _u32, _u32, _ptr]),
     "mb_read_sum": (_i32, [_i32, _ptr, _ptr, _u64, _u32, _u32, _ptr]),
     "mb_tensor_peak_configs": (_i32, [_i32, ctypes.POINTER(PeakConfig), _i32]),
@@ -167,6 +169,28 @@ def device_query(device: int) -> dict:
     call("mb_device_query", device, ctypes.byref(info))
     return {field: (getattr(info, field).decode(errors="replace") if isinstance(getattr(info, field), bytes)
                     else getattr(info, field)) for field, _ in DeviceInfo._fields_ if field != "reserved0"}
+
+
+def wall_clock_khz() -> int:
+    """Rate of the device's constant real-time counter (the clock witness's time base), in kHz."""
+    khz = ctypes.c_int(0)
+    call("mb_wall_clock_khz", ctypes.byref(khz))
+    return khz.value
+
+
+def clock_witness(out, microseconds: int, stream=None) -> None:
+    """Enqueue the one-wave engine-clock witness on `stream` (a torch stream; default: the current one).
+
+    out: int64 device tensor of 4 entries; after the stream completes it holds shader clock cycles, real-time
+    ticks, polls and the starting real-time count (mb_clock_witness).
+    """
+    import torch
+
+    if out.dtype != torch.int64 or out.numel() < 4 or not out.is_cuda or not out.is_contiguous():
+        raise ValueError("clock witness output must be a contiguous int64 device tensor of 4 entries")
+    handle = (stream or torch.cuda.current_stream()).cuda_stream
+    call("mb_clock_witness", ctypes.c_void_p(out.data_ptr()), out.numel() * 8, int(microseconds),
+         ctypes.c_void_p(handle))
 
 
 def kernel_names() -> list[str]:

@@ -27,7 +27,7 @@ MATRIX_MNEMONICS = ("v_mfma_", "v_wmma_", "v_mmac_")
 # arguments are recovered from its Itanium-mangled name.
 _MFMA_FORMAT = {"MfmaBf16": "bf16", "MfmaF16": "f16", "MfmaI8": "i8", "MfmaFp8": "fp8",
                 "MfmaMxfp4": "mxfp4", "MfmaF32": "f32", "MfmaF64": "f64"}
-_PEAK_RE = re.compile(r"tensor_peak_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
+_PEAK_RE = re.compile(r"tensor_peak_(?:tied_)?kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
 _GEMM_RE = re.compile(r"gemm_kernelINS_\d+(Mfma\w+?)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E")
 _GEMM_STAGED_RE = re.compile(r"gemm_(?:staged|dma)_kernelINS_\d+(Mfma\w+?)EE")
 _ELEM_BITS = {"bf16": 16, "f16": 16, "i8": 8, "fp8": 8, "mxfp4": 4, "f32": 32, "f64": 64}
@@ -68,6 +68,8 @@ def registered_name(symbol: str) -> str | None:
     if match:
         kind, unroll = match.groups()
         return f"vector_{kind}_u{unroll}"
+    if "clock_witness_kernel" in symbol:
+        return "clock_witness"
     if "copy_tail_kernel" in symbol:
         return "copy_tail"
     return None

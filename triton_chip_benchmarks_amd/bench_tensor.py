@@ -488,6 +488,9 @@ def build_parser():
     parser.add_argument("--b-layout", choices=("kn", "nk", "both"), default="kn",
                         help="peak B tile layout: [K][N] (reference default), [N][K], or both")
     parser.add_argument("--tiles", nargs="+", help="restrict peak tiles, e.g. 128x128x64")
+    parser.add_argument("--inputs", choices=("baseline", "reference"), default="baseline",
+                        help="GEMM operands: the benchmark configuration's sets (default), or the reference's own "
+                             "recipe (N(0,1) A, N(0,1)/sqrt(K) B, INT8 {-1,0,1}; sizes 2048 4096 8192)")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--quick", action="store_true",
                         help="smoke test: one tile and 64 repeats, or GEMM dimensions 256/544")

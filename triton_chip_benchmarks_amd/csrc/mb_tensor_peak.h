@@ -189,10 +189,153 @@ __global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
   }
 }
 
+// The same computation with the 16x16 instructions issued in place
+// (Op::mma_tied) on AGPR accumulators, for tiles whose 16x16 accumulators
+// fill the AGPR file (256x256 per four waves: 256 registers per lane). The
+// builtin forms of these instructions get accumulator copies (and spills) at
+// that size, so the compiler cannot be left to allocate them.
+//
+// The compiler does not see the inline-assembly MFMAs, so the kernel keeps
+// their hazard distances itself:
+//   * every operand fragment is a plain LDS read (ds_read_b128), whose waits
+//     the compiler inserts for any reader; B is therefore stored transposed
+//     in LDS ([BN][BK] bytes) whatever its layout in HBM;
+//   * consecutive updates of one accumulator are MFMAs writing exactly the
+//     same registers, which the hardware orders;
+//   * ordered fences on every accumulator (acc_hazard_fence) separate the
+//     zeroing from the first MFMA and the last MFMA from the stores.
+// Unscaled formats only (the scaled MXFP4 instruction takes its scales in
+// VGPRs, which this kernel does not stage).
+template <class Op, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int CHAINS, bool B_NK>
+__global__ void __launch_bounds__(64 * WAVES_M * WAVES_N)
+    tensor_peak_tied_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                            const uint8_t* __restrict__, const uint8_t* __restrict__,
+                            typename Op::Out* __restrict__ C, uint32_t blocks, uint32_t iterations) {
+  using T = PeakTile<Op, BM, BN, BK, WAVES_M, WAVES_N, CHAINS, B_NK>;
+  static_assert(Op::M == 16 && !Op::SCALED, "in-place tiles use the unscaled 16x16 instructions");
+  static_assert(T::ELEM_BYTES == 1 || T::ELEM_BYTES == 2, "B is transposed in LDS element by element");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[T::A_BYTES + CHAINS * T::B_BYTES];
+  const uint64_t block = blockIdx.x;
+
+  typename Op::Acc acc[CHAINS][T::TM][T::TN];
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn) acc[c][tm][tn] = typename Op::Acc{};
+
+  // Stage A[block] as it is, and every B[c][block] as [BN][BK] bytes.
+  const uint8_t* a_src = A + block * T::A_BYTES;
+  for (int i = threadIdx.x * 16; i < T::A_BYTES; i += T::THREADS * 16)
+    *reinterpret_cast<i32x4*>(lds + i) = *reinterpret_cast<const i32x4*>(a_src + i);
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c) {
+    const uint8_t* b_src = B + (static_cast<uint64_t>(c) * blocks + block) * T::B_BYTES;
+    uint8_t* b_dst = lds + T::A_BYTES + c * T::B_BYTES;
+    for (int i = threadIdx.x * 16; i < T::B_BYTES; i += T::THREADS * 16) {
+      const i32x4 v = *reinterpret_cast<const i32x4*>(b_src + i);
+      if constexpr (B_NK) {
+        *reinterpret_cast<i32x4*>(b_dst + i) = v;
+      } else {
+        // Byte offset i of [BK][BN] holds element (k, n) = (i / row, (i % row) / ELEM_BYTES)
+        // with row = BN * ELEM_BYTES; it goes to (n * BK + k) * ELEM_BYTES.
+        constexpr int E = T::ELEM_BYTES, ROW = BN * E, PER = 16 / E;
+        const int k = i / ROW, n0 = (i % ROW) / E;
+        if constexpr (E == 2) {
+          const auto h = __builtin_bit_cast(uint16_t __attribute__((ext_vector_type(8))), v);
+#pragma unroll
+          for (int e = 0; e < PER; ++e) *reinterpret_cast<uint16_t*>(b_dst + ((n0 + e) * BK + k) * E) = h[e];
+        } else {
+          const auto h = __builtin_bit_cast(uint8_t __attribute__((ext_vector_type(16))), v);
+#pragma unroll
+          for (int e = 0; e < PER; ++e) b_dst[(n0 + e) * BK + k] = h[e];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int lrow = lane % Op::M, lgroup = lane / Op::M;
+  constexpr int KB = MfmaGeometry<Op>::K_BYTES;
+
+  typename Op::Frag a[T::TM][T::KSTEPS];
+  typename Op::Frag b[CHAINS][T::TN][T::KSTEPS];
+#pragma unroll
+  for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+    for (int ks = 0; ks < T::KSTEPS; ++ks) {
+      const int row = wm * T::WM + tm * Op::M + lrow;
+      a[tm][ks] = load_frag<typename Op::Frag>(lds + row * T::BK_BYTES + ks * KB + lgroup * Op::LANE_BYTES);
+    }
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+      for (int ks = 0; ks < T::KSTEPS; ++ks) {
+        const int col = wn * T::WN + tn * Op::N + lrow;
+        b[c][tn][ks] = load_frag<typename Op::Frag>(lds + T::A_BYTES + c * T::B_BYTES + col * T::BK_BYTES +
+                                                    ks * KB + lgroup * Op::LANE_BYTES);
+      }
+  // lgkmcnt(0) (vmcnt and expcnt fields at their maxima): every fragment is in
+  // its registers before the loop, so no wait is left inside it.
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn) acc_hazard_fence(acc[c][tm][tn]);
+
+  for (uint32_t it = 0; it < iterations; ++it) {
+#pragma unroll
+    for (int ks = 0; ks < T::KSTEPS; ++ks)
+#pragma unroll
+      for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+        for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < T::TN; ++tn) Op::mma_tied(a[tm][ks], b[c][tn][ks], acc[c][tm][tn]);
+  }
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn) acc_hazard_fence(acc[c][tm][tn]);
+
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c) {
+    typename Op::Out* out = C + (static_cast<uint64_t>(c) * blocks + block) * BM * BN;
+#pragma unroll
+    for (int tm = 0; tm < T::TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < T::TN; ++tn)
+#pragma unroll
+        for (int r = 0; r < Op::ACC_REGS; ++r) {
+          const int row = wm * T::WM + tm * Op::M + Op::out_row(lane, r);
+          const int col = wn * T::WN + tn * Op::N + (lane % Op::N);
+          out[row * BN + col] = acc[c][tm][tn][r];
+        }
+  }
+}
+
 template <class Op, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int CHAINS, bool B_NK>
 void launch_peak(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c,
                  uint32_t blocks, uint32_t iterations, hipStream_t stream) {
   tensor_peak_kernel<Op, BM, BN, BK, WAVES_M, WAVES_N, CHAINS, B_NK>
+      <<<dim3(blocks), dim3(64 * WAVES_M * WAVES_N), 0, stream>>>(
+          a, b, sa, sb, static_cast<typename Op::Out*>(c), blocks, iterations);
+}
+
+template <class Op, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int CHAINS, bool B_NK>
+void launch_peak_tied(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const uint8_t* sb, void* c,
+                      uint32_t blocks, uint32_t iterations, hipStream_t stream) {
+  tensor_peak_tied_kernel<Op, BM, BN, BK, WAVES_M, WAVES_N, CHAINS, B_NK>
       <<<dim3(blocks), dim3(64 * WAVES_M * WAVES_N), 0, stream>>>(
           a, b, sa, sb, static_cast<typename Op::Out*>(c), blocks, iterations);
 }
@@ -214,4 +357,17 @@ void launch_peak(const uint8_t* a, const uint8_t* b, const uint8_t* sa, const ui
 #define MB_PEAK_BOTH(FMT, OP, BM, BN, BK, WM, WN, CH, NAME)             \
   MB_PEAK(FMT, OP, BM, BN, BK, WM, WN, CH, false, NAME "_kn"),          \
       MB_PEAK(FMT, OP, BM, BN, BK, WM, WN, CH, true, NAME "_nk")
+
+// In-place (tensor_peak_tied_kernel) variants, both B layouts.
+#define MB_PEAK_TIED(FMT, OP, BM, BN, BK, WM, WN, CH, NK, NAME)                                              \
+  PeakVariant{FMT,                                                                                           \
+              mb_peak_config{BM, BN, BK, CH, NK, OP::M, 64 * WM * WN},                                       \
+              NAME,                                                                                          \
+              reinterpret_cast<const void*>(tensor_peak_tied_kernel<OP, BM, BN, BK, WM, WN, CH, NK>),        \
+              launch_peak_tied<OP, BM, BN, BK, WM, WN, CH, NK>,                                              \
+              static_cast<int>(sizeof(typename OP::Out)),                                                    \
+              OP::ELEM_BITS}
+#define MB_PEAK_TIED_BOTH(FMT, OP, BM, BN, BK, WM, WN, CH, NAME)        \
+  MB_PEAK_TIED(FMT, OP, BM, BN, BK, WM, WN, CH, false, NAME "_kn"),     \
+      MB_PEAK_TIED(FMT, OP, BM, BN, BK, WM, WN, CH, true, NAME "_nk")
 

@@ -21,10 +21,14 @@ const PeakVariant kPeakVariants[] = {
     MB_PEAK_BOTH(MB_MATRIX_MXFP4, MfmaMxfp4, 64, 64, 128, 2, 2, 2, "tensor_peak_mxfp4_64x64x128_c2"),
     MB_PEAK_BOTH(MB_MATRIX_MXFP4, MfmaMxfp4, 128, 128, 256, 2, 2, 2, "tensor_peak_mxfp4_128x128x256_c2"),
     MB_PEAK_BOTH(MB_MATRIX_MXFP4, MfmaMxfp4, 256, 256, 256, 2, 2, 1, "tensor_peak_mxfp4_256x256x256_c1"),
-    // 16x16-instruction form (suffix _mfma16) of the 256x256 FP8 tile; the
-    // 128x128 ones are in mb_tensor_peak_vgpr.hip, and the other 256x256 ones
-    // spill or copy accumulators inside the loop and are not built.
+    // 16x16-instruction forms (suffix _mfma16) of the 256x256 tiles: FP8's
+    // builtin keeps its accumulators in place; BF16, FP16 and INT8 issue the
+    // in-place form (tensor_peak_tied_kernel). The 128x128 ones are in
+    // mb_tensor_peak_vgpr.hip; MXFP4's 256x256 16x16 form is not built.
     MB_PEAK_BOTH(MB_MATRIX_FP8_E4M3, MfmaFp8x16, 256, 256, 128, 2, 2, 1, "tensor_peak_fp8_256x256x128_c1_mfma16"),
+    MB_PEAK_TIED_BOTH(MB_MATRIX_BF16, MfmaBf16x16, 256, 256, 64, 2, 2, 1, "tensor_peak_bf16_256x256x64_c1_mfma16"),
+    MB_PEAK_TIED_BOTH(MB_MATRIX_F16, MfmaF16x16, 256, 256, 64, 2, 2, 1, "tensor_peak_f16_256x256x64_c1_mfma16"),
+    MB_PEAK_TIED_BOTH(MB_MATRIX_I8, MfmaI8x16, 256, 256, 64, 2, 2, 1, "tensor_peak_i8_256x256x64_c1_mfma16"),
     MB_PEAK_BOTH(MB_MATRIX_F32, MfmaF32, 64, 64, 32, 2, 2, 2, "tensor_peak_f32_64x64x32_c2"),
     MB_PEAK_BOTH(MB_MATRIX_F32, MfmaF32, 128, 128, 32, 2, 2, 2, "tensor_peak_f32_128x128x32_c2"),
     MB_PEAK_BOTH(MB_MATRIX_F64, MfmaF64, 32, 32, 16, 2, 2, 2, "tensor_peak_f64_32x32x16_c2"),
