@@ -25,7 +25,11 @@
 extern "C" {
 #endif
 
-#define MB_ABI_VERSION 1
+/* Version 2: mb_gemm takes MXFP4 scales in K-step blocks [ceil(k/256)][rows][8]
+ * (version 1 took them row-major, [rows][k/32]). The two have the same byte
+ * count when k is a multiple of 256, so a caller built for version 1 must not
+ * load this library: check mb_abi_version() first. */
+#define MB_ABI_VERSION 2
 
 #define MB_OK 0
 #define MB_ERR_INVALID (-1)     /* bad argument: size, shape, configuration */
@@ -110,6 +114,17 @@ int mb_clock_witness(uint64_t* out, uint64_t out_bytes, uint32_t microseconds, v
  * Replaces: bench_bandwidth.py:36-47 (copy_kernel, launch_copy). */
 int mb_copy(const void* src, void* dst, uint64_t bytes, uint32_t block_threads,
             uint32_t vectors_per_thread, uint32_t grid_blocks, uint32_t flags, void* stream);
+
+/* Every 32-bit word of dst[0:bytes) = `pattern` (byte i of a tail shorter
+ * than 16 bytes = byte i % 4 of the little-endian pattern): the copy's store
+ * stream alone, one 16-byte store per lane, `flags` as for mb_copy (store
+ * policy only). dst must be 16-byte aligned. `grid_blocks` = 0 launches one
+ * workgroup per `block_threads` vectors; otherwise that many stride over dst.
+ * No counterpart in the reference, which measures copy and read only: with
+ * mb_read_sum it gives the write-only and read-only HBM rates that bound a
+ * copy, which mixes the two. */
+int mb_fill(void* dst, uint64_t bytes, uint32_t pattern, uint32_t block_threads, uint32_t grid_blocks,
+            uint32_t flags, void* stream);
 
 /* Element types understood by mb_read_sum. */
 #define MB_DTYPE_F32 0

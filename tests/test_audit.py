@@ -123,6 +123,7 @@ def test_registered_names_follow_the_mangled_template_arguments():
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_119gemm_dma_f64_kernelINS_7MfmaF64EEEvPKh") \
         == "gemm_f64_256x128x16"
     assert audit.registered_name("_ZN2mb12_GLOBAL__N_117vector_f16_kernelILi8EEEv") == "vector_f16_u8"
+    assert audit.registered_name("_ZN2mb12_GLOBAL__N_111fill_kernelILi2EEEvPDv4_jmj") == "fill_dwordx4_stream"
     assert audit.registered_name("unrelated_symbol") is None
 
 

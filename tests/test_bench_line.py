@@ -40,7 +40,12 @@ def _fake_rows():
             "clock": {"clock_mhz": 2011.123, "witness_ms": 100.0, "polls": 753762, "load_launches": 200,
                       "method": "mb_clock_witness: s_memtime cycles / s_memrealtime ticks of one wave beside the "
                                 "kernel's launches"},
+            "power": {"mean_w": 1399.87654, "seconds": 2.0000001, "host_seconds": 2.0001, "updates": 3,
+                      "cap_w": 1400.0, "method": "m" * 200},
             "frac_at_clock": 0.97, "config": {"text": "c" * 400}, "validation": "v" * 1500})
+        if name == "hbm_copy":
+            rows[-1].update(rw_bound_frac=0.88765432, frac_of_rw_bound=0.9567891,
+                            context={"read_only_gbps": 7123.456789, "method": "m" * 300})
     return rows
 
 

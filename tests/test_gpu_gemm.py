@@ -256,6 +256,44 @@ def test_mxfp4_gemm_applies_each_rows_group_scale(gpu):
             assert np.array_equal(got, expected), f"max error {np.abs(got - expected).max()}"
 
 
+def test_mxfp4_gemm_reads_the_block_scale_layout_not_row_major(gpu):
+    """The scale layout is ABI (version 2): the K-step blocks [K/256][rows][8]. Row-major [rows][K/32]
+    scales have the same byte count whenever K is a multiple of 256, so the size check cannot catch a
+    caller still using them; this pins what such a call computes. Passing the row-major bytes gives the
+    oracle product of those bytes read as blocks (so the kernel reads exactly the documented layout), and
+    differs from the correctly scaled product (so the mix-up is visible, not hidden by unit scales)."""
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+
+    assert _native.load().mb_abi_version() == 2
+    rng = np.random.default_rng(29)
+    config = max(_configs("fp4"), key=lambda c: c["tile_m"] * c["tile_n"])
+    m, n, k = config["tile_m"], config["tile_n"], 4 * 256
+    print(f"gemm fp4 scale layout {m}x{n}x{k}", flush=True)
+    codes_a = rng.integers(0, 16, (m, k), dtype=np.uint8)
+    codes_b = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    sa = rng.integers(126, 129, (m, k // 32), dtype=np.uint8)
+    sb = rng.integers(126, 129, (n, k // 32), dtype=np.uint8)
+    a = torch.from_numpy(ot.pack_e2m1(codes_a)).cuda()
+    b = torch.from_numpy(ot.pack_e2m1(codes_b)).cuda()
+
+    def product(scale_a_rows, scale_b_rows):
+        return ot.gemm_reference(ot.e2m1_decode(codes_a) * np.repeat(ot.e8m0_decode(scale_a_rows), 32, axis=1),
+                                 (ot.e2m1_decode(codes_b) * np.repeat(ot.e8m0_decode(scale_b_rows), 32, axis=1)).T)
+
+    def as_rows(blocks):  # bytes read as [K/256][rows][8] -> the [rows][K/32] scales they mean
+        return np.ascontiguousarray(blocks.transpose(1, 0, 2)).reshape(blocks.shape[1], -1)
+
+    c = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    _native.gemm("fp4", config, a, b, c, m, n, k, torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda())
+    torch.cuda.synchronize()
+    got = c.cpu().numpy().astype(np.float64)
+    misread = product(as_rows(sa.reshape(k // 256, m, 8)), as_rows(sb.reshape(k // 256, n, 8)))
+    assert np.array_equal(got, misread)
+    assert not np.array_equal(got, product(sa, sb))
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32", "fp64", "int8"])
 def test_reference_recipe_ragged_shape_matches_oracle(gpu, dtype):
     """The reference's own operands (bench_tensor.py:249-261: N(0,1) A, N(0,1)/sqrt(K) B drawn [K][N], INT8

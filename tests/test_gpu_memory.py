@@ -118,3 +118,55 @@ def test_read_exact_on_integer_lattice(gpu):
     torch.cuda.synchronize()
     expected = memory.block_sums(values.cpu().numpy(), 4096)
     assert np.array_equal(sink.cpu().numpy().astype(np.float64), expected)
+
+
+@pytest.mark.parametrize("nbytes", [1, 15, 16, 17, 4096 + 9, (1 << 22) + 3])
+@pytest.mark.parametrize("threads,grid_blocks,policy", [(64, 0, "stream"), (256, 0, "off"), (1024, 0, "on"),
+                                                        (256, 3, "stream")])
+def test_fill_writes_every_byte_and_nothing_past_the_end(gpu, nbytes, threads, grid_blocks, policy):
+    """mb_fill: every byte of a ragged buffer holds its byte of the little-endian pattern (the 16-byte body
+    and the byte tail), and the guard bytes after the buffer are untouched; a small grid strides over all."""
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+    from triton_chip_benchmarks_amd.bench_bandwidth import COPY_POLICIES
+
+    print(f"fill bytes={nbytes} threads={threads} grid={grid_blocks} policy={policy}", flush=True)
+    pattern = 0xA1B2C3D4
+    buffer = torch.full((nbytes + 64,), 0x5A, dtype=torch.uint8, device="cuda")
+    _native.call("mb_fill", buffer.data_ptr(), nbytes, pattern, threads, grid_blocks, COPY_POLICIES[policy],
+                 _native.stream_handle())
+    torch.cuda.synchronize()
+    host = buffer.cpu().numpy()
+    expected = np.frombuffer(np.array([pattern], dtype="<u4").tobytes(), dtype=np.uint8)[np.arange(nbytes) % 4]
+    assert np.array_equal(host[:nbytes], expected)
+    assert (host[nbytes:] == 0x5A).all()
+
+
+def test_fill_refuses_bad_arguments(gpu):
+    import torch
+
+    from triton_chip_benchmarks_amd import _native
+
+    library = _native.load()
+    buffer = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    assert library.mb_fill(None, 16, 0, 64, 0, 0, None) == _native.MB_ERR_INVALID
+    assert library.mb_fill(buffer.data_ptr() + 4, 16, 0, 64, 0, 0, None) == _native.MB_ERR_ALIGNMENT
+    assert library.mb_fill(buffer.data_ptr(), 16, 0, 65, 0, 0, None) == _native.MB_ERR_INVALID
+    assert library.mb_fill(buffer.data_ptr(), 16, 0, 64, 0, 8, None) == _native.MB_ERR_INVALID
+    assert "mb_fill" in _native.last_error()
+    assert library.mb_fill(buffer.data_ptr(), 0, 0, 64, 0, 0, None) == _native.MB_OK
+
+
+def test_fill_baseline_size_full_buffer(gpu):
+    """The write-only leg of the copy bound at the copy's size: 2^28 fp32 words all 1.0 afterwards."""
+    import torch
+
+    from triton_chip_benchmarks_amd.bench_bandwidth import check_fill, launch_fill
+
+    print("fill 2^28 fp32", flush=True)
+    dst = torch.full((1 << 28,), float("nan"), device="cuda")
+    launch_fill(dst, 256, 0, "stream")
+    torch.cuda.synchronize()
+    check_fill(dst)
+    assert bool((dst == 1.0).all())

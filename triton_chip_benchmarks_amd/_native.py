@@ -13,7 +13,7 @@ import threading
 
 PACKAGE = Path(__file__).resolve().parent
 LIBRARY_PATH = PACKAGE / "libmi355x_bench.so"
-ABI_VERSION = 1
+ABI_VERSION = 2  # 2: MXFP4 GEMM scales in K-step blocks (mb_gemm)
 
 MB_OK = 0
 MB_ERR_INVALID = -1
@@ -96,6 +96,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mb_wall_clock_khz": (_i32, [ctypes.POINTER(_i32)]),
     "mb_clock_witness": (_i32, [_ptr, _u64, _u32, _ptr]),
     "mb_copy": (_i32, [_ptr, _ptr, _u64, _u32, _u32, _u32, _u32, _ptr]),
+    "mb_fill": (_i32, [_ptr, _u64, _u32, _u32, _u32, _u32, _ptr]),
     "mb_read_sum": (_i32, [_i32, _ptr, _ptr, _u64, _u32, _u32, _ptr]),
     "mb_tensor_peak_configs": (_i32, [_i32, ctypes.POINTER(PeakConfig), _i32]),
     "mb_tensor_peak_kernel_name": (ctypes.c_char_p, [_i32, ctypes.POINTER(PeakConfig)]),

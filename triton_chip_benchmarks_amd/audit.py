@@ -72,6 +72,11 @@ def registered_name(symbol: str) -> str | None:
         return "clock_witness"
     if "copy_tail_kernel" in symbol:
         return "copy_tail"
+    match = re.search(r"fill_kernelILi([0-2])EEEv", symbol)
+    if match:
+        return "fill_dwordx4" + ("", "_nt", "_stream")[int(match.group(1))]
+    if "fill_tail_kernel" in symbol:
+        return "fill_tail"
     return None
 
 

@@ -71,6 +71,34 @@ def launch_copy(src, dst, block_threads, vectors_per_thread, grid_blocks=0, nont
                  grid_blocks, COPY_POLICIES[copy_policy(nontemporal)], _native.stream_handle())
 
 
+FILL_PATTERN = 0x3F800000  # every fp32 word 1.0
+
+
+def launch_fill(dst, block_threads, grid_blocks=0, policy="stream", pattern=FILL_PATTERN):
+    """Every 32-bit word of dst <- pattern through mb_fill (the copy's store stream alone)."""
+    _native.call("mb_fill", dst.data_ptr(), dst.numel() * dst.element_size(), pattern, block_threads, grid_blocks,
+                 COPY_POLICIES[copy_policy(policy)], _native.stream_handle())
+
+
+def check_fill(dst, pattern=FILL_PATTERN):
+    """Every word of a filled buffer holds the pattern (bit-exact)."""
+    import torch
+
+    words = dst.view(torch.int32)
+    signed = pattern - (1 << 32) if pattern >= 1 << 31 else pattern
+    bad = int((words != signed).sum())
+    if bad:
+        raise AssertionError(f"Write validation failed: {bad} of {words.numel()} words differ from 0x{pattern:08x}")
+    return {"correctness": "passed (every word equals the fill pattern)"}
+
+
+def rw_bound(read_gbps, write_gbps):
+    """Rate of a copy that moves equal read and write bytes, each at its own measured rate, with nothing lost
+    to switching between them: the harmonic mean of the two. A copy mixes both streams on the same HBM
+    channels, so this bounds it from above."""
+    return 2.0 / (1.0 / read_gbps + 1.0 / write_gbps)
+
+
 def launch_read(src, sink, block_size, block_threads):
     """sink[i] <- sum of src block i, through mb_read_sum."""
     segments = -(-src.numel() // block_size)
@@ -132,8 +160,10 @@ def cache_regime(buffer_bytes, cache_bytes, quick):
 def parse_args(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     add_common_arguments(parser)
-    parser.add_argument("--mode", choices=["copy", "read", "all"], default="all",
-                        help="Access patterns to measure separately (default: all)")
+    parser.add_argument("--mode", choices=["copy", "read", "write", "all", "bound"], default="all",
+                        help="Access patterns to measure separately: all = copy and read (default); write = "
+                             "the copy's store stream alone (mb_fill); bound = copy, read and write, plus "
+                             "the read/write bound of a copy")
     parser.add_argument("--sizes-mib", type=positive_int, nargs="+", default=[256, 512, 1024, 2048],
                         help="Size of EACH source/destination buffer in MiB")
     parser.add_argument("--dtype", choices=["fp16", "bf16", "fp32"], default="fp32")
@@ -183,7 +213,7 @@ def main(argv=None):
     dtype = torch_dtype(args.dtype)
     element_size = torch.empty((), dtype=dtype).element_size()
     cache_bytes = metadata["l2_cache_bytes"]
-    modes = ["copy", "read"] if args.mode == "all" else [args.mode]
+    modes = {"all": ["copy", "read"], "bound": ["copy", "read", "write"]}.get(args.mode, [args.mode])
     configs = configurations(args, element_size)
     generator = torch.Generator(device=device)
 
@@ -198,6 +228,11 @@ def main(argv=None):
                             nontemporal)
                 if not torch.equal(small_src, small_dst):
                     raise AssertionError(f"Copy tail validation failed: block={block}, warps={config['num_warps']}")
+        if "write" in modes:
+            for policy in config["nontemporal"]:
+                small_dst = torch.full_like(small_src, float("nan"))
+                launch_fill(small_dst, threads, args.grid_blocks, policy)
+                check_fill(small_dst)
         if "read" in modes:
             small_sink = torch.full((-(-small_src.numel() // block),), float("nan"), device=device)
             launch_read(small_src, small_sink, block, threads)
@@ -222,16 +257,30 @@ def main(argv=None):
             print(f"Note: {size_mib} MiB per buffer excluded from the HBM-sized peak summary: {reason}.")
         generator.manual_seed(args.seed)
         src = torch.empty(n, device=device, dtype=dtype).uniform_(-1, 1, generator=generator)
-        dst = torch.empty_like(src) if "copy" in modes else None
+        dst = torch.empty_like(src) if "copy" in modes or "write" in modes else None
+        written = set()  # (threads, policy) of the write rows: the block size does not change a fill
         for config in configs:
             block, warps, threads = config["block_size"], config["num_warps"], config["block_threads"]
             for mode in modes:
-                variants = config["nontemporal"] if mode == "copy" else [None]
+                variants = config["nontemporal"] if mode in ("copy", "write") else [None]
                 if mode == "copy" and config["vectors_per_thread"] is None:
                     continue  # step size does not split into whole 16-byte lanes
                 for nontemporal in variants:
                     sink = None
-                    if mode == "copy":
+                    if mode == "write":
+                        if (threads, nontemporal) in written:
+                            continue
+                        written.add((threads, nontemporal))
+                        dst.fill_(float("nan"))
+
+                        def run(threads=threads, policy=nontemporal):
+                            launch_fill(dst, threads, args.grid_blocks, policy)
+
+                        run()
+                        correctness = check_fill(dst)
+                        write_bytes = buffer_bytes
+                        kernel = f"fill_dwordx4{POLICY_SUFFIX[copy_policy(nontemporal)]}"
+                    elif mode == "copy":
                         per_thread = config["vectors_per_thread"]
                         dst.fill_(float("nan"))
 
@@ -256,17 +305,21 @@ def main(argv=None):
                         write_bytes = sink.numel() * sink.element_size()
                         kernel = f"read_sum_{args.dtype}_vec"
                     timings = measure(run, args)
-                    traffic = buffer_bytes + write_bytes
+                    traffic = write_bytes if mode == "write" else buffer_bytes + write_bytes
                     gbps = traffic / (timings["median_ms"] * 1e6)
                     peak_gbps = traffic / (timings["min_ms"] * 1e6)
                     row = {"mode": f"device_global_memory_{mode}", "pattern": mode, "dtype": args.dtype,
                            "buffer_mib": size_mib, "buffer_bytes": buffer_bytes, "elements": n,
-                           "read_bytes": buffer_bytes, "write_bytes": write_bytes, "traffic_bytes": traffic,
+                           "read_bytes": 0 if mode == "write" else buffer_bytes, "write_bytes": write_bytes,
+                           "traffic_bytes": traffic,
                            "block_size": block, "num_warps": warps, "block_threads": threads,
                            "kernel": kernel, "cache_regime": regime, "peak_eligible": peak_eligible,
                            "smoke_only": args.quick, **timings, "gbps": gbps, "tbps": gbps / 1000,
                            "peak_gbps": peak_gbps, "peak_tbps": peak_gbps / 1000,
                            "fraction_of_hbm_peak": peak_gbps / roofline.HBM_PEAK_GBPS, **correctness}
+                    if mode == "write":
+                        row.update(cache_policy=copy_policy(nontemporal), grid_blocks=args.grid_blocks,
+                                   pattern_word=f"0x{FILL_PATTERN:08x}")
                     if mode == "copy":
                         row.update(vectors_per_thread=config["vectors_per_thread"],
                                    nontemporal=copy_policy(nontemporal) != "off",
@@ -290,6 +343,13 @@ def main(argv=None):
         print(f"{label} {mode} bandwidth: {best['peak_gbps']:.2f} GB/s ({best['peak_tbps']:.3f} TB/s, "
               f"{100 * best['fraction_of_hbm_peak']:.1f}% of 8 TB/s), {best['buffer_mib']} MiB/buffer, "
               f"block={best['block_size']}, warps={best['num_warps']}.")
+    best = {mode: max((row["peak_gbps"] for row in (eligible or rows) if row["pattern"] == mode), default=None)
+            for mode in ("copy", "read", "write")}
+    if all(best.values()):
+        bound = rw_bound(best["read"], best["write"])
+        print(f"Read/write bound of a copy (harmonic mean of the best read and write rates): {bound:.2f} GB/s "
+              f"({100 * bound / roofline.HBM_PEAK_GBPS:.1f}% of 8 TB/s); the best copy reaches "
+              f"{100 * best['copy'] / bound:.1f}% of it.")
     if not eligible:
         print("No HBM-sized peak candidate: eligibility requires buffers >= 4x the last-level cache "
               "and a run without --quick.")
