@@ -447,3 +447,32 @@ def test_read_check_agrees_with_the_oracle_on_whole_and_tail_blocks(block):
     broken = sums.copy()
     broken[1] = np.nan
     assert verdicts(broken) == (False, False)
+
+
+def test_summary_tie_breaks_rejections_and_row_shape():
+    """Equal peaks keep the first configuration (its median with it); a run whose rows all declared
+    `unsupported` is unsupported, a mixed or empty one an error with the distinct reasons in order; a declared
+    status keeps the child's reason even when it is None; the memory row lists its patterns copy, then read."""
+    item = metric("tensor_bf16")
+    compiled = {"execution_kind": "tensor", "native_tensor_verified": True, "instruction_precision_verified": True}
+    tie = summarize(item, {"results": [{"peak_tflops": 100, "tflops": 90, "block_size": 1, "compiled": compiled},
+                                       {"peak_tflops": 100, "tflops": 95, "block_size": 2, "compiled": compiled},
+                                       {"peak_tflops": 0, "tflops": 99}]})
+    assert (tie["value"], tie["median_value"], tie["configuration"]["block_size"]) == (100, 90, 1)
+    assert tie["successful_configurations"] == 2
+    unsupported = summarize(item, {"results": [{"status": "unsupported", "reason": "a"},
+                                               {"status": "unsupported", "reason": "b"}, "not a row"]})
+    assert (unsupported["status"], unsupported["reason"]) == ("unsupported", "a; b")
+    mixed = summarize(item, {"results": [{"status": "unsupported", "reason": "a"}, {"status": "error", "reason": "b"},
+                                         {"status": "error", "reason": "a"}]})
+    assert (mixed["status"], mixed["reason"]) == ("error", "a; b")
+    empty = summarize(item, {"results": []})
+    assert (empty["status"], empty["reason"]) == ("error", "Benchmark produced no valid throughput measurements")
+    assert summarize(item, {"results": {}})["reason"] == "Benchmark results must be a list"
+    declared = summarize(item, {"status": "error", "reason": None})
+    assert "reason" in declared and declared["reason"] is None and declared["status"] == "error"
+    memory = summarize(metric("memory_bandwidth"), {"results": [
+        {"pattern": "read", "peak_gbps": 7000, "gbps": 6900, "peak_eligible": True},
+        {"pattern": "copy", "peak_gbps": 6800, "gbps": 6700, "peak_eligible": True}]})
+    assert list(memory["patterns"]) == ["copy", "read"]
+    assert list(memory)[:7] == ["metric", "group", "precision", "unit", "status", "value", "median_value"]

@@ -115,63 +115,91 @@ def summarize(metric, document):
     return result
 
 
-def _summarize(metric, document):
-    """One report row from a child's result document.
+# Child statuses that are reported as they are, without looking at measurements.
+_DECLARED_STATUSES = frozenset(("unsupported", "not_implemented", "error", "unavailable"))
+# The memory row's per-pattern record: which patterns are kept, and which of them may set the row value.
+_MEMORY_PATTERNS = ("copy", "read")
+_MEMORY_VALUE_PATTERN = "copy"
+_NO_HBM_COPY = ("No HBM-sized copy candidate: use a non-quick run with known last-level cache capacity "
+                "and buffers at least 4x that capacity; observed pattern rates remain in patterns")
 
-    A declared status (unsupported, not_implemented, error, unavailable) is
-    kept as is. Otherwise the best valid row wins; failures are errors unless
-    every rejected configuration was itself declared unsupported.
-    """
-    result = empty_metric(metric)
+
+@dataclass(frozen=True)
+class _Candidate:
+    """One child row with both rates positive: (peak, median) in the metric's unit."""
+    peak: float
+    median: float
+    row: dict
+
+    @property
+    def hbm_sized(self) -> bool:
+        return self.row.get("peak_eligible") is True and not self.row.get("smoke_only", False)
+
+
+def _candidates(metric, rows):
+    """(valid candidates, rejected dict rows): a row is valid when its status is ok and both rates are positive."""
+    valid, rejected = [], []
+    for row in rows:
+        if not isinstance(row, dict):
+            continue
+        rejected.append(row)
+        peak, median = rates(metric, row)
+        if row.get("status", "ok") == "ok" and _positive(peak) and _positive(median):
+            valid.append(_Candidate(peak, median, row))
+    return valid, rejected
+
+
+def _best(candidates):
+    """The highest peak; the first of equal peaks (its median comes from the same configuration)."""
+    return max(candidates, key=lambda candidate: candidate.peak)
+
+
+def _declared(metric, document):
     status = document.get("status")
-    if status in ("unsupported", "not_implemented", "error", "unavailable"):
-        result.update(status=status, reason=document.get("reason", status))
-        widened = (document.get("details") or {}).get("widened") if isinstance(document.get("details"), dict) else None
-        if isinstance(widened, dict):
-            # A converted (widened) measurement is a detail of the row, never its value.
-            result["widened_measurement"] = widened
-        return result
-    if metric.key == "memory_capacity":
-        capacity = document.get("device", {}).get("total_memory_bytes")
-        if _positive(capacity):
-            result.update(status="ok", value=capacity / 2**30, capacity_bytes=capacity,
-                          measurement_kind="reported_device_capacity")
-        else:
-            result.update(status="unavailable", reason="Backend did not report total memory capacity")
-        return result
+    if status not in _DECLARED_STATUSES:
+        return None
+    result = empty_metric(metric)
+    result.update(status=status, reason=document.get("reason", status))  # kept even when the child gave None
+    details = document.get("details")
+    widened = details.get("widened") if isinstance(details, dict) else None
+    if isinstance(widened, dict):
+        # A converted (widened) measurement is a detail of the row, never its value.
+        result["widened_measurement"] = widened
+    return result
 
+
+def _capacity(metric, document):
+    if metric.key != "memory_capacity":
+        return None
+    capacity = document.get("device", {}).get("total_memory_bytes")
+    if not _positive(capacity):
+        return empty_metric(metric, "unavailable", "Backend did not report total memory capacity")
+    result = empty_metric(metric, "ok")
+    result.update(value=capacity / 2**30, capacity_bytes=capacity, measurement_kind="reported_device_capacity")
+    return result
+
+
+def _measured(metric, document):
     rows = document.get("results", [])
     if not isinstance(rows, list):
         return empty_metric(metric, "error", "Benchmark results must be a list")
-    valid = [row for row in rows if isinstance(row, dict) and row.get("status", "ok") == "ok"
-             and all(_positive(value) for value in rates(metric, row))]
+    valid, rejected = _candidates(metric, rows)
     if not valid:
-        rejected = [row for row in rows if isinstance(row, dict)]
-        unsupported = bool(rejected) and all(row.get("status") == "unsupported" for row in rejected)
-        reasons = list(dict.fromkeys(str(row.get("reason", "No valid throughput")) for row in rejected))
-        return empty_metric(metric, "unsupported" if unsupported else "error",
+        # Every rejected configuration declared unsupported -> the row is unsupported; anything else is an error.
+        status = "unsupported" if rejected and all(row.get("status") == "unsupported" for row in rejected) else "error"
+        reasons = dict.fromkeys(str(row.get("reason", "No valid throughput")) for row in rejected)
+        return empty_metric(metric, status,
                             "; ".join(reasons) or "Benchmark produced no valid throughput measurements")
-
+    result = empty_metric(metric)
     if metric.key == "memory_bandwidth":
-        patterns = {}
-        for pattern in ("copy", "read"):
-            candidates = [row for row in valid if row.get("pattern") == pattern]
-            eligible = [row for row in candidates
-                        if row.get("peak_eligible") is True and not row.get("smoke_only", False)]
-            if candidates:
-                best = max(eligible or candidates, key=lambda row: rates(metric, row)[0])
-                patterns[pattern] = _details(metric, best)
-        result["patterns"] = patterns
-        valid = [row for row in valid if row.get("pattern") == "copy"
-                 and row.get("peak_eligible") is True and not row.get("smoke_only", False)]
+        by_pattern = {pattern: [c for c in valid if c.row.get("pattern") == pattern] for pattern in _MEMORY_PATTERNS}
+        result["patterns"] = {pattern: _details(metric, _best([c for c in group if c.hbm_sized] or group).row)
+                              for pattern, group in by_pattern.items() if group}
+        valid = [c for c in by_pattern[_MEMORY_VALUE_PATTERN] if c.hbm_sized]
         if not valid:
-            result.update(status="not_measured", reason=(
-                "No HBM-sized copy candidate: use a non-quick run with known last-level cache capacity "
-                "and buffers at least 4x that capacity; observed pattern rates remain in patterns"))
+            result.update(status="not_measured", reason=_NO_HBM_COPY)
             return result
-
-    best = max(valid, key=lambda row: rates(metric, row)[0])
-    result.update(status="ok", **_details(metric, best))
+    result.update(status="ok", **_details(metric, _best(valid).row))
     if document.get("arguments", {}).get("quick") and metric.group != "Memory":
         result["smoke_only"] = True
     reason = _verification_reason(metric, result)
@@ -181,38 +209,80 @@ def _summarize(metric, document):
     return result
 
 
+# Stages in order; the first that returns a row decides it.
+_STAGES = (_declared, _capacity, _measured)
+
+
+def _summarize(metric, document):
+    """One report row from a child's result document (suite_report.py:88-148).
+
+    A declared status (unsupported, not_implemented, error, unavailable) is
+    kept as is; capacity comes from the device block; otherwise the highest
+    valid peak wins, with its own configuration's median, and a run with no
+    valid row is an error unless every rejected configuration declared itself
+    unsupported.
+    """
+    for stage in _STAGES:
+        result = stage(metric, document)
+        if result is not None:
+            return result
+    raise AssertionError("the last stage always returns a row")
+
+
+def _number(value, digits=3):
+    return "-" if value is None else f"{value:.{digits}f}"
+
+
+# Table columns: (header, width, alignment, cell). Notes: (rule, message) pairs applied to every row in order.
+_COLUMNS = (
+    ("Metric", 20, "<", lambda item: item["metric"]),
+    ("Peak / capacity", 17, ">", lambda item: _number(item.get("value"))),
+    ("Median", 12, ">", lambda item: _number(item.get("median_value"))),
+    ("Unit", 8, "<", lambda item: item["unit"]),
+    ("% peak", 7, ">", lambda item: _number(None if (item.get("roofline") or {}).get("frac") is None
+                                            else 100 * item["roofline"]["frac"], 1)),
+    ("Status", 0, "<", lambda item: item["status"]),
+)
+
+
+def _widened_note(item):
+    widened = item.get("widened_measurement")
+    if isinstance(widened, dict) and widened.get("peak_tflops"):
+        return (f"widened ({widened.get('arithmetic_kind', 'converted')}) {widened['peak_tflops']:.3f} TFLOP/s "
+                "- not native arithmetic, not the row value")
+    return None
+
+
+_NOTES = (
+    lambda item: item.get("reason") or None,
+    lambda item: "smoke test; not a peak result" if item.get("smoke_only") else None,
+    _widened_note,
+    lambda item: ("measured matrix rate using SIMT scalar/vector instructions (no native tensor MMA)"
+                  if item.get("execution_kind") == "simt" else None),
+)
+
+
+def _line(cells):
+    return " ".join(f"{cell:{align}{width}}" if width else cell
+                    for cell, (_, width, align, _) in zip(cells, _COLUMNS))
+
+
 def format_table(results):
-    """One line per requested metric, including missing ones, then notes."""
-    lines = [f"{'Metric':<20} {'Peak / capacity':>17} {'Median':>12} {'Unit':<8} {'% peak':>7} Status",
-             "-" * 94]
-    notes = []
-    for item in results:
-        value = "-" if item.get("value") is None else f"{item['value']:.3f}"
-        median = "-" if item.get("median_value") is None else f"{item['median_value']:.3f}"
-        frac = (item.get("roofline") or {}).get("frac")
-        percent = "-" if frac is None else f"{100 * frac:.1f}"
-        lines.append(f"{item['metric']:<20} {value:>17} {median:>12} {item['unit']:<8} {percent:>7} "
-                     f"{item['status']}")
-        if item.get("reason"):
-            notes.append(f"{item['metric']}: {item['reason']}")
-        if item.get("smoke_only"):
-            notes.append(f"{item['metric']}: smoke test; not a peak result")
-        widened = item.get("widened_measurement")
-        if isinstance(widened, dict) and widened.get("peak_tflops"):
-            notes.append(f"{item['metric']}: widened ({widened.get('arithmetic_kind', 'converted')}) "
-                         f"{widened['peak_tflops']:.3f} TFLOP/s - not native arithmetic, not the row value")
-        if item.get("execution_kind") == "simt":
-            notes.append(f"{item['metric']}: measured matrix rate using SIMT scalar/vector instructions "
-                         "(no native tensor MMA)")
+    """One line per requested metric (missing ones included), then the host baselines, then notes."""
+    header = _line([title for title, *_ in _COLUMNS])
+    lines = [header, "-" * (len(header) + 8)]
+    lines += [_line([cell(item) for *_, cell in _COLUMNS]) for item in results]
+    notes = [f"{item['metric']}: {note}" for item in results for rule in _NOTES
+             for note in (rule(item),) if note]
     baselines = [item for item in results if isinstance(item.get("cpu_baseline"), dict)]
     if baselines:
-        host = baselines[0]["cpu_baseline"].get("host") or {}
-        lines.extend(("", f"Host CPU baseline (the reference's host computation, {host.get('cpu_model') or 'CPU'}, "
-                          f"{baselines[0]['cpu_baseline'].get('cores')} threads):"))
-        for item in baselines:
-            baseline = item["cpu_baseline"]
-            lines.append(f"  {item['metric']:<20} {baseline['value']:>12.4g} {baseline['unit']:<8} "
-                         f"{baseline.get('method', '')}; {baseline.get('sample', '')}")
+        first = baselines[0]["cpu_baseline"]
+        host = first.get("host") or {}
+        lines += ["", f"Host CPU baseline (the reference's host computation, {host.get('cpu_model') or 'CPU'}, "
+                      f"{first.get('cores')} threads):"]
+        lines += [f"  {item['metric']:<20} {item['cpu_baseline']['value']:>12.4g} {item['cpu_baseline']['unit']:<8} "
+                  f"{item['cpu_baseline'].get('method', '')}; {item['cpu_baseline'].get('sample', '')}"
+                  for item in baselines]
     if notes:
-        lines.extend(("", *notes))
+        lines += ["", *notes]
     return "\n".join(lines)
