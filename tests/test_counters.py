@@ -169,3 +169,65 @@ def test_optional_stall_and_path_passes(tmp_path):
     assert gemm["td_stalled_by_l1_frac"] == pytest.approx(0.2)
     # Neither pass runs by default.
     assert "stall" not in counters.DEFAULT_PASSES and "path" not in counters.DEFAULT_PASSES
+
+
+def test_registered_names_of_in_place_tiles_fill_and_untemplated_kernels():
+    assert counters.registered_name(
+        "void mb::(anonymous namespace)::tensor_peak_tied_kernel<mb::MfmaBf16x16, 256, 256, 64, 2, 2, 1, false>"
+        "(unsigned char const*, unsigned char const*, unsigned char const*, unsigned char const*, float*, "
+        "unsigned int, unsigned int)") == "tensor_peak_bf16_256x256x64_c1_mfma16_kn"
+    assert counters.registered_name(
+        "void mb::(anonymous namespace)::fill_kernel<2>(unsigned int __vector(4)*, unsigned long, unsigned int)") \
+        == "fill_dwordx4_stream"
+    assert counters.registered_name(
+        "mb::(anonymous namespace)::clock_witness_kernel(unsigned long*, unsigned long, unsigned long)") \
+        == "clock_witness"
+
+
+def _trace_csv(path, dispatches):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with path.open("w") as stream:
+        stream.write("Kind,Dispatch_Id,Kernel_Name,Start_Timestamp,End_Timestamp\n")
+        for index, (name, start, end) in enumerate(dispatches):
+            stream.write(f'KERNEL_DISPATCH,{index},"{name}",{start},{end}\n')
+
+
+def test_trace_report_finds_each_rows_timed_run(tmp_path):
+    """The timed launches of a row are the first run of exactly `steps` dispatches of its kernel after the previous
+    row's: longer warmup and load runs are skipped, and two rows sharing a kernel take its runs in order."""
+    poison = "void at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<float> >(int)"
+    dispatches, t = [], 0.0
+
+    def run(name, count, ms):
+        nonlocal t
+        for _ in range(count):
+            dispatches.append((name, t, t + ms * 1e6))
+            t += ms * 1e6 + 1000
+
+    run(COPY, 40, 0.3)          # warmup
+    run(poison, 1, 0.01)
+    run(COPY, 3, 0.32)          # timed (steps = 3)
+    run(GEMM, 10, 0.7)          # warmup of row 2
+    run(poison, 1, 0.01)
+    run(GEMM, 3, 0.72)          # timed
+    run(poison, 1, 0.01)
+    run(GEMM, 3, 0.74)          # a second row on the same kernel
+    _trace_csv(tmp_path / "host" / "1" / "run_kernel_trace.csv", dispatches)
+    detail = {"steps": 3, "rows": [{"name": "hbm_copy", "kernel": "copy_dwordx4_vpt1_stream", "ms_per_launch": 0.33},
+                                   {"name": "gemm_a", "kernel": "gemm_bf16_256x256x64", "ms_per_launch": 0.72},
+                                   {"name": "gemm_b", "kernel": "gemm_bf16_256x256x64", "ms_per_launch": 0.74}]}
+    text = counters.trace_report(counters.load_trace(tmp_path), detail)
+    assert "| hbm_copy | `copy_dwordx4_vpt1_stream` | 0.3200 | 0.3300 | +3.12% |" in text
+    assert "| gemm_a | `gemm_bf16_256x256x64` | 0.7200 | 0.7200 | +0.00% |" in text
+    assert "| gemm_b | `gemm_bf16_256x256x64` | 0.7400 | 0.7400 | +0.00% |" in text
+    assert "| `copy_dwordx4_vpt1_stream` | 43 |" in text
+
+
+def test_traffic_table_lists_measured_kernels_in_row_order():
+    summary = {"fetch_size_bytes_per_byte": 0.5000154, "write_size_bytes_per_byte": 1.0,
+               "kernels": {"copy_dwordx4_vpt1_stream": {"hbm_bytes": 2147483648.4},
+                           "gemm_bf16_256x256x64": {"hbm_bytes": 1.88e9}, "unmeasured": {}}}
+    text = counters.traffic_table(summary, ["copy_dwordx4_vpt1_stream", "unmeasured", "gemm_bf16_256x256x64"], "cmd")
+    body = [line for line in text.splitlines() if not line.startswith("#")]
+    assert body == ["copy_dwordx4_vpt1_stream = 2147483648", "gemm_bf16_256x256x64 = 1880000000"]
+    assert "FETCH_SIZE / 0.5000154" in text and "# Made by: cmd" in text

@@ -111,9 +111,13 @@ def registered_name(demangled: str) -> str:
             return name
     parsed = _template(demangled) if "mb::" in demangled else None
     if parsed is None:
+        if "mb::" in demangled:  # untemplated library kernels: clock_witness_kernel, copy_tail_kernel, ...
+            bare = demangled.replace("void ", "").replace("(anonymous namespace)::", "")
+            base = re.sub(r"\(.*$", "", bare).rsplit("::", 1)[-1]
+            return base.removesuffix("_kernel")
         return re.sub(r"\(.*$", "", demangled.replace("void ", ""))[:120]
     family, args = parsed[0], [part.replace("mb::", "") for part in parsed[1]]
-    if family == "tensor_peak_kernel":
+    if family in ("tensor_peak_kernel", "tensor_peak_tied_kernel"):
         fmt, bm, bn, bk, _wm, _wn, chains, nk = args
         shape = "_mfma16" if fmt.endswith("x16") else ""
         return (f"tensor_peak_{_MFMA_FORMAT[fmt.removesuffix('x16')]}_{bm}x{bn}x{bk}_c{chains}{shape}_"
@@ -133,6 +137,8 @@ def registered_name(demangled: str) -> str:
     if family == "read_sum_kernel":
         kind = {"float": "f32", "_Float16": "f16", "__bf16": "bf16"}.get(args[0], args[0])
         return f"read_sum_{kind}{'_vec' if args[1] != '1' else ''}"
+    if family == "fill_kernel":
+        return "fill_dwordx4" + {"0": "", "1": "_nt", "2": "_stream"}.get(args[0], "")
     if family.startswith("vector_") and family.endswith("_kernel"):
         return f"{family[:-len('_kernel')]}_u{args[0]}"
     return family
@@ -392,6 +398,88 @@ def target(report_path: Path, launches: int, selected=None) -> None:
         torch.cuda.synchronize()
 
 
+# ---- HBM traffic table read by bench.py -------------------------------------------
+
+def traffic_table(summary: dict, kernels, command: str) -> str:
+    """`kernel = bytes` lines (HBM read + write per launch) for the given kernels, with the derivation."""
+    lines = ["# HBM-side bytes per launch (read + write) of the bench.py kernels at bench.py's",
+             "# launch shapes, from rocprofv3 FETCH_SIZE and WRITE_SIZE counter runs (KiB per",
+             "# dispatch), each scaled by what the same counter reads for the 1 GiB plain copy",
+             f"# in the same run (FETCH_SIZE / {summary['fetch_size_bytes_per_byte']:.7f}, "
+             f"WRITE_SIZE / {summary['write_size_bytes_per_byte']:.7f}).",
+             f"# Made by: {command}"]
+    for kernel in kernels:
+        row = summary["kernels"].get(kernel) or {}
+        if row.get("hbm_bytes") is not None:
+            lines.append(f"{kernel} = {round(row['hbm_bytes'])}")
+    return "\n".join(lines) + "\n"
+
+
+# ---- kernel trace of a bench.py run ---------------------------------------------
+
+def load_trace(directory: Path) -> list[tuple[float, float, str]]:
+    """(start ns, end ns, registry name) of every dispatch in a rocprofv3 --kernel-trace run, by start time."""
+    found = sorted(directory.rglob("*kernel_trace.csv"))
+    if not found:
+        raise SystemExit(f"no *kernel_trace.csv under {directory}")
+    dispatches = []
+    for path in found:
+        with path.open() as stream:
+            for record in csv.DictReader(stream):
+                dispatches.append((float(record["Start_Timestamp"]), float(record["End_Timestamp"]),
+                                   registered_name(record["Kernel_Name"])))
+    return sorted(dispatches)
+
+
+def trace_report(dispatches, detail: dict) -> str:
+    """Per-kernel statistics of the trace, then each bench.py row's timed launches against its own figure.
+
+    A row's timed launches are the first run, after the previous row's, of exactly `steps` consecutive
+    dispatches of the row's kernel: its warmup, clock-witness load and power load are longer runs, and the
+    witness kernel or the output poisoning separates them.
+    """
+    steps = int(detail["steps"])
+    total = sum(end - start for start, end, _ in dispatches)
+    per_kernel: dict[str, list[float]] = {}
+    for start, end, name in dispatches:
+        per_kernel.setdefault(name, []).append((end - start) / 1e6)
+    rows = detail["rows"]
+    ours = {row["kernel"] for row in rows}
+    lines = ["| kernel (registry name) | calls | average ms | min ms | max ms | share of GPU time |",
+             "|---|---:|---:|---:|---:|---:|"]
+    other = 0.0
+    for name, times in sorted(per_kernel.items(), key=lambda item: -sum(item[1])):
+        if name not in ours:
+            other += sum(times)
+            continue
+        lines.append(f"| `{name}` | {len(times)} | {sum(times) / len(times):.4f} | {min(times):.4f} | "
+                     f"{max(times):.4f} | {100 * sum(times) * 1e6 / total:.2f}% |")
+    lines += ["", f"All other kernels (input generation, reference products, validation, the copy's read and "
+                  f"write legs, outside the timed regions): {100 * other * 1e6 / total:.2f}% of GPU time.", ""]
+    runs, current = [], None
+    for start, end, name in dispatches:
+        if current and current[0] == name:
+            current[1].append((end - start) / 1e6)
+        else:
+            current = (name, [(end - start) / 1e6])
+            runs.append(current)
+    lines += [f"| row | kernel | rocprofv3 mean ms ({steps} timed) | bench.py ms_per_launch | difference |",
+              "|---|---|---:|---:|---:|"]
+    position = 0
+    for row in rows:
+        match = next((i for i in range(position, len(runs))
+                      if runs[i][0] == row["kernel"] and len(runs[i][1]) == steps), None)
+        if match is None:
+            lines.append(f"| {row['name']} | `{row['kernel']}` | not found | {row['ms_per_launch']:.4f} | — |")
+            continue
+        position = match + 1
+        traced = sum(runs[match][1]) / steps
+        difference = round(100 * (row["ms_per_launch"] / traced - 1), 2) + 0.0  # + 0.0: no "-0.00"
+        lines.append(f"| {row['name']} | `{row['kernel']}` | {traced:.4f} | {row['ms_per_launch']:.4f} | "
+                     f"{difference:+.2f}% |")
+    return "\n".join(lines) + "\n"
+
+
 # ---- CLI ---------------------------------------------------------------------
 
 def main(argv=None) -> int:
@@ -413,6 +501,14 @@ def main(argv=None) -> int:
     p.add_argument("--markdown", type=Path)
     p.add_argument("--by-grid", action="store_true",
                    help="keep launches of one kernel over different grids apart (kernel@<workgroups>wg)")
+    p = sub.add_parser("trace", help="kernel-trace statistics of a bench.py run and its timed launches")
+    p.add_argument("--trace-dir", type=Path, required=True, help="rocprofv3 -d directory of the run")
+    p.add_argument("--detail", type=Path, required=True, help="bench.py --detail file of the same run")
+    p.add_argument("--markdown", type=Path)
+    p = sub.add_parser("traffic", help="bench.py's HBM traffic table from a counter summary")
+    p.add_argument("--summary", type=Path, required=True, help="counters summarize --json output")
+    p.add_argument("--detail", type=Path, required=True, help="a bench.py --detail file naming the row kernels")
+    p.add_argument("--write", type=Path, required=True)
     p = sub.add_parser("attach", help="copy kernel summaries into a report's rows")
     p.add_argument("--summary", type=Path, required=True)
     p.add_argument("--report", type=Path, required=True)
@@ -429,6 +525,18 @@ def main(argv=None) -> int:
         if args.json:
             args.json.write_text(json.dumps(summary, indent=2) + "\n")
         text = markdown(summary)
+        if args.markdown:
+            args.markdown.write_text(text)
+        print(text)
+    elif args.command == "traffic":
+        detail = json.loads(args.detail.read_text())
+        kernels = list(dict.fromkeys(row["kernel"] for row in detail["rows"]))
+        command = " ".join(["python -m triton_chip_benchmarks_amd.counters", *(argv or sys.argv[1:])])
+        text = traffic_table(json.loads(args.summary.read_text()), kernels, command)
+        args.write.write_text(text)
+        print(text)
+    elif args.command == "trace":
+        text = trace_report(load_trace(args.trace_dir), json.loads(args.detail.read_text()))
         if args.markdown:
             args.markdown.write_text(text)
         print(text)
