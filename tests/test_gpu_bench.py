@@ -18,6 +18,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT))
 TOP_LEVEL = {"metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
              "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline", "rows"}
 
@@ -70,6 +71,17 @@ def test_bench_prints_one_contract_line(gpu, tmp_path):
         assert compact[name]["clock_mhz"] == round(row["clock"]["clock_mhz"])
         if row["bound"] != "hbm":
             assert row["frac_at_clock"] < 1.03, (name, row["frac_at_clock"])
+    # The copy row carries its read/write bound, measured on its own buffers, which a copy cannot beat by more
+    # than timing noise.
+    copy = rows["hbm_copy"]
+    assert 0.5 < copy["rw_bound_frac"] < 1.0 and copy["frac"] <= 1.05 * copy["rw_bound_frac"], copy["context"]
+    assert compact["hbm_copy"]["rw_bound_frac"] == pytest.approx(copy["rw_bound_frac"], rel=1e-3)
+    if line["config"]["power_cap_w"] is not None:  # the ROCm SMI library saw the device: metered rows carry power
+        import bench
+
+        for name in bench.POWER_ROWS:
+            assert 100 < rows[name]["power"]["mean_w"] < 2000, (name, rows[name]["power"])
+            assert compact[name]["power_w"] == round(rows[name]["power"]["mean_w"])
     for row in rows.values():
         assert row["min_ms_per_launch"] <= row["median_ms_per_launch"] * (1 + 1e-9)
         assert row["warmup_device_ms"] >= 30 * 0.99 and "timed launches" in row["validation"]
