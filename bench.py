@@ -117,8 +117,8 @@ MAX_LINE_BYTES = 8192
 CLOCK_WITNESS_MS = 100.0
 CLOCK_LOAD_MS = 150.0
 # Rows whose board power is measured, and the load that measurement needs: the board's energy counter updates
-# once a second, so the row's kernel runs back to back for POWER_LOAD_MS around the clock witness and the mean
-# power is taken between the first and last counter updates inside that load.
+# once a second, so in a pass after every row is timed, each of these kernels runs back to back for
+# POWER_LOAD_MS and the mean power is taken between the first and last counter updates inside that load.
 POWER_ROWS = ("hbm_copy", "peak_bf16", "gemm_bf16", "gemm_fp16", "gemm_fp8", "gemm_int8", "gemm_fp64", "gemm_mxfp4",
               "peak_mxfp4")
 POWER_LOAD_MS = 2300.0
@@ -504,7 +504,7 @@ class PowerMeter:
     def __init__(self, torch):
         self.handle, self.cap_w, self._thread, self._samples = None, None, None, []
         try:
-            sys.path.append("/opt/rocm/share/amd_smi")
+            sys.path.append(os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "share", "amd_smi"))
             import amdsmi
 
             amdsmi.amdsmi_init()

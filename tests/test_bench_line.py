@@ -104,3 +104,28 @@ def test_rounding_keeps_significant_digits():
     assert bench._round(0.000123456789) == pytest.approx(0.00012346)
     assert bench._round(None) is None and bench._round(7) == 7
     assert math.isnan(bench._round(float("nan")))
+
+
+def test_power_meter_takes_the_mean_between_counter_updates_inside_the_load():
+    """stop(): the first sample is the counter as found (its last update precedes the load) and is skipped; the
+    power is the energy difference (uJ) over the time-stamp difference (ns) of the first and last updates after it;
+    fewer than two updates give no figure."""
+    import threading
+
+    meter = bench.PowerMeter.__new__(bench.PowerMeter)
+    meter.cap_w = 1400.0
+
+    def stopped(samples):
+        meter._samples, meter._stop = samples, threading.Event()
+        meter._thread = threading.Thread(target=lambda: None)
+        meter._thread.start()
+        return meter.stop()
+
+    found = (5.0e9, 1_000_000_000, 0.0)
+    updates = [(5.0e9 + 1.4e9, 2_000_000_000, 1.0), (5.0e9 + 2.8e9, 3_000_000_000, 2.0),
+               (5.0e9 + 4.2e9, 4_000_000_000, 3.0)]
+    result = stopped([found, *updates])
+    assert result["mean_w"] == pytest.approx(1400.0) and result["seconds"] == pytest.approx(2.0)
+    assert result["updates"] == 3 and result["cap_w"] == 1400.0 and result["host_seconds"] == pytest.approx(2.0)
+    assert stopped([found, updates[0]]) is None
+    assert stopped([]) is None
