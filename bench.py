@@ -740,7 +740,12 @@ def full_document(args, info, rows, cpu_rows, host) -> dict:
                       "achieved": dominant["value"], "peak": dominant["peak"], "unit": dominant["unit"],
                       "frac": dominant["frac"], "traffic": dominant["traffic_bytes_per_launch"],
                       "algorithmic_work_per_launch": dominant["algorithmic_work_per_launch"],
-                      "work_unit": dominant["work_unit"], "ms_per_launch": dominant["ms_per_launch"]}
+                      "work_unit": dominant["work_unit"], "ms_per_launch": dominant["ms_per_launch"],
+                      # The conditions it ran under: its engine clock (witness), the fraction at that clock, and the
+                      # board power its kernel draws (None where not measured).
+                      "clock_mhz": (dominant.get("clock") or {}).get("clock_mhz"),
+                      "frac_at_clock": dominant.get("frac_at_clock"),
+                      "power_w": (dominant.get("power") or {}).get("mean_w")}
     cpu = None
     if cpu_rows:
         in_mean = [r for r in cpu_rows if r["name"] in HEADLINE] or cpu_rows

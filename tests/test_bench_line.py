@@ -129,3 +129,13 @@ def test_power_meter_takes_the_mean_between_counter_updates_inside_the_load():
     assert result["updates"] == 3 and result["cap_w"] == 1400.0 and result["host_seconds"] == pytest.approx(2.0)
     assert stopped([found, updates[0]]) is None
     assert stopped([]) is None
+
+
+def test_roofline_block_carries_the_dominant_kernels_clock_and_power():
+    line = bench.headline_line(_fake_document(), "results/bench_detail.json")
+    dominant = max((r for r in _fake_rows() if r["in_headline"]), key=lambda r: r["ms_per_launch"])
+    roofline = line["roofline"]
+    assert roofline["kernel"] == dominant["kernel"] and roofline["row"] == dominant["name"]
+    assert roofline["clock_mhz"] == pytest.approx(dominant["clock"]["clock_mhz"], rel=1e-4)
+    assert roofline["frac_at_clock"] == pytest.approx(dominant["frac_at_clock"], rel=1e-4)
+    assert roofline["power_w"] == pytest.approx(dominant["power"]["mean_w"], rel=1e-4)
